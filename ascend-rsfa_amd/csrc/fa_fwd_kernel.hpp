@@ -1,0 +1,513 @@
+// FlashAttention-2 forward for MI355X (gfx950 / CDNA4), hand-written HIP.
+//
+// Reference algorithm: Dell710000/ascend-rsfa ascend_rsfa/flash_attention_forward.py
+//   _attn_fwd (271-404), _attn_fwd_inner (163-226), _attn_fwd_split_inner
+//   (408-489), causal prefix/diagonal split (338-368, 493-541).
+//
+// Work decomposition
+//   One task = (batch b, head h, query block mb) of BM = 32*NW query rows.
+//   A workgroup of NW wave64s runs tasks from a persistent queue; wave w owns
+//   the 32 query rows [mb*BM + 32w, +32).  K and V stream through LDS in tiles
+//   of BN keys, double buffered: tile j+1 is fetched with direct global->LDS
+//   loads (global_load_lds_dwordx4) while tile j is computed.
+//
+// Contractions (v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulation)
+//   S^T = K Q^T : A = K rows from LDS (ds_read_b128), B = Q^T kept in VGPRs for
+//                 the whole task.  In the 32x32 accumulator layout lane l holds
+//                 query column l%32 and keys 8*(r/4) + 4*(l/32) + r%4 in its 16
+//                 registers r, so every query row lives in one lane pair
+//                 (l, l^32): the row max needs one permlane32 swap, the row sum
+//                 none until the end of the task.
+//   O^T = V^T P^T : B = P^T converted in registers straight from the S^T
+//                 accumulator (no LDS round trip); A = V^T read with the gfx950
+//                 transposing LDS load ds_read_b64_tr_b16 from the same
+//                 row-major V tile, with keys ordered to match P^T's registers.
+//                 O^T's layout puts each query in one lane too, so the online
+//                 softmax rescale is a per-lane multiply.
+//
+// Online softmax (exp2 domain, c = |sm_scale| * log2 e)
+//   m_tile = c * rowmax(S); the running max is only moved when the tile max
+//   exceeds it by more than RESCALE_SLACK (log2 units), so most tiles skip the
+//   O rescale entirely (the reference's FA4-style skip, 466-487, uses slack 0;
+//   any slack gives the same softmax, it only bounds P <= 2^slack).  P is
+//   rounded to the input dtype before the PV product, as the reference does
+//   (211, 456); the row sum adds the rounded values (v_dot2 with ones).
+//
+// LDS layout of one K or V tile (BN rows x DP cols, 2-byte elements)
+//   rows are grouped in blocks of 16; inside a block the 16-byte chunk c of row
+//   r sits at  c*256 + ((r%16) ^ (4*(c%4)))*16.  Each 256-byte chunk plane holds
+//   16 rows, so a half-wave's 16-byte K reads and the 16-lane groups of the
+//   transposing V reads both touch 64 distinct banks, and one wave's direct
+//   load instruction fills 1 KB of consecutive LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace rsfa {
+
+#define RSFA_LDS __attribute__((address_space(3)))
+#define RSFA_GLOBAL __attribute__((address_space(1)))
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// How far (in log2 units) the running row max may lag the true max before the
+// accumulator is rescaled.  P = 2^(s*c - m) stays <= 2^8, exact in fp16/bf16
+// range; the final normalisation divides it out.
+constexpr float RESCALE_SLACK = 8.0f;
+
+struct TypeF16 {
+    typedef _Float16 elem;
+    typedef _Float16 x8 __attribute__((ext_vector_type(8)));
+    typedef _Float16 x4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+    typedef decltype(__builtin_amdgcn_ds_read_tr16_b64_v4f16(nullptr)) tr4;
+    static __device__ __forceinline__ f32x16 mfma(x8 a, x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ tr4 tr_read(const RSFA_LDS char* p) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4f16((RSFA_LDS tr4*)p);
+    }
+    static __device__ __forceinline__ x2 cvt2(float a, float b) {
+        return __builtin_convertvector((f32x2){a, b}, x2);
+    }
+    static __device__ __forceinline__ float dot2(x2 a, x2 b, float c) {
+        return __builtin_amdgcn_fdot2(a, b, c, false);
+    }
+    static __device__ __forceinline__ x2 ones2() { return (x2){(elem)1.0f, (elem)1.0f}; }
+};
+
+struct TypeBF16 {
+    typedef __bf16 elem;
+    typedef __bf16 x8 __attribute__((ext_vector_type(8)));
+    typedef __bf16 x4 __attribute__((ext_vector_type(4)));
+    typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+    typedef decltype(__builtin_amdgcn_ds_read_tr16_b64_v4bf16(nullptr)) tr4;
+    static __device__ __forceinline__ f32x16 mfma(x8 a, x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ tr4 tr_read(const RSFA_LDS char* p) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((RSFA_LDS tr4*)p);
+    }
+    static __device__ __forceinline__ x2 cvt2(float a, float b) {
+        return __builtin_convertvector((f32x2){a, b}, x2);
+    }
+    static __device__ __forceinline__ float dot2(x2 a, x2 b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+    }
+    static __device__ __forceinline__ x2 ones2() { return (x2){(elem)1.0f, (elem)1.0f}; }
+};
+
+// Kernel modes.  MODE_FUSED runs every key tile of a task in one launch (the
+// causal prefix with the mask-free body, the diagonal with the masked body).
+// MODE_PREFIX / MODE_DIAG are the reference's two-launch causal split
+// (STAGE 4 / STAGE 5, flash_attention_forward.py:338-368).
+enum { MODE_FUSED = 0, MODE_PREFIX = 1, MODE_DIAG = 2 };
+
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;      // optional [Z*H, n_ctx]
+    float* state;    // split mode: [2][Z*H*nmb*BM] (m, l) per query row
+    int64_t q_sz, q_sh, q_sm;
+    int64_t k_sz, k_sh, k_sn;
+    int64_t v_sz, v_sh, v_sn;
+    int64_t o_sz, o_sh, o_sm;
+    int32_t H;
+    int32_t n_ctx;
+    int32_t nmb;        // query blocks per head = ceil(n_ctx / BM)
+    int32_t num_heads;  // Z * H
+    int32_t num_tasks;  // num_heads * nmb
+    int32_t group;      // causal: heads per heavy-first group
+    float c;            // |sm_scale| * log2(e)
+    uint32_t neg;       // 1 when sm_scale < 0: q is negated (exact) and c = |c|
+    uint32_t* ticket;   // dynamic queue counter (returns to 0 at kernel end) or null
+};
+
+__device__ __forceinline__ float swap_max(float x) {
+    // {x[l%32], x[l%32 + 32]} in some order for every lane l
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float swap_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Task order.  Non-causal: head-major, so consecutive tickets share K/V in L2.
+// Causal: heads in groups of p.group, inside a group the heaviest query blocks
+// first (longest-processing-time first), which bounds the tail of the
+// persistent grid while keeping a group's K/V resident.
+template <bool CAUSAL>
+__device__ __forceinline__ void decode_task(const FwdParams& p, int t, int& bh, int& mb) {
+    if (!CAUSAL) {
+        bh = t / p.nmb;
+        mb = t - bh * p.nmb;
+    } else {
+        const int per_group = p.group * p.nmb;
+        const int g = t / per_group;
+        const int w = t - g * per_group;
+        const int g0 = g * p.group;
+        const int gc = min(p.group, p.num_heads - g0);
+        const int i = w / gc;
+        mb = p.nmb - 1 - i;
+        bh = g0 + (w - i * gc);
+    }
+}
+
+// One wave's direct global->LDS load: each lane fetches 16 bytes from
+// sbase + voff_bytes and the hardware writes lane i's data to
+// lds_addr + 16*i (1 KB of consecutive LDS per instruction).  It is issued from
+// inline asm so the compiler does not make later LDS reads wait for it; the
+// kernel itself waits (vmcnt(0) + barrier) before reading a buffer a load
+// targets, and only ever loads into the buffer nobody is reading.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff_bytes, uint32_t lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff_bytes), "s"(sbase), "{m0}"(lds_addr)
+                 : "memory");
+}
+
+__device__ __forceinline__ void wait_loads_and_sync() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+}
+
+template <class T, int D, int BN, int NW, bool CAUSAL, int MODE, int OCC>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
+fa_fwd_kernel(FwdParams p) {
+    typedef typename T::elem elem;
+    typedef typename T::x8 x8;
+    typedef typename T::x4 x4;
+    typedef typename T::x2 x2;
+
+    constexpr int DP = D < 32 ? 32 : D;  // LDS row width / PV output rows
+    constexpr int KST = D / 16;          // 16-wide k-steps of QK^T
+    constexpr int DT = DP / 32;          // 32-row tiles of O^T
+    constexpr int CPR = DP / 8;          // 16-byte chunks per LDS row
+    constexpr int CPRV = D / 8;          // chunks that hold data
+    constexpr int NKT = BN / 32;         // 32-key sub-tiles of a key tile
+    constexpr int BM = NW * 32;
+    constexpr int BLK = 32 * DP;          // bytes of a 16-row block
+    constexpr int TILE = BN * DP * 2;     // bytes of one K (or V) tile
+    constexpr int BUF = 2 * TILE;         // K + V
+    constexpr int NINST = BN * CPR / 64;  // 1-KB direct loads per tile
+    static_assert(BN % 32 == 0 && BN >= 32, "BN must be a multiple of 32");
+    static_assert(D % 16 == 0, "D must be a multiple of 16");
+    static_assert((BN * CPR) % 64 == 0, "tile must be whole 1-KB load slices");
+    static_assert(MODE == MODE_FUSED || CAUSAL, "split modes are causal only");
+
+    __shared__ __attribute__((aligned(1024))) char smem_raw[2 * BUF];
+    __shared__ int s_ticket;
+    RSFA_LDS char* const smem = (RSFA_LDS char*)smem_raw;
+    const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int hh = lane >> 5;  // which 8-key half of a 16-key MFMA step
+    const int l32 = lane & 31;
+    const int l16 = lane & 15;
+
+    // LDS read offsets (bytes, relative to a K or V tile).
+    // K (A operand of S^T): row l32 (+32 per sub-tile), chunk 2s+hh.
+    uint32_t koff[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) koff[e] = (l32 >> 4) * BLK + hh * 256 + ((l16 ^ (8 * e + 4 * hh)) * 16);
+    // V (A operand of O^T via transposing reads): lane l16 of a 16-lane group
+    // addresses row (l16/4) of the group's 4 keys and columns 4*(l16%4)..+3 of
+    // its 16 head dims; the hardware hands lane j column j of the 4 rows.
+    const int vg = (lane >> 4) & 1;
+    const int vcc = 2 * vg + ((l16 >> 1) & 1);
+    uint32_t voff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        voff[u] = vcc * 256 + (((8 * u + 4 * hh + (l16 >> 2)) ^ (4 * vcc)) * 16) + 8 * (l16 & 1);
+
+    // Loader: in every 1-KB slice lane i fills chunk 4*cg + i/16 of the 16-row
+    // block's row (i%16) ^ 4*((i/16)%4), so its global offset inside the block
+    // is the same for every slice.
+    const int ld_rib = l16 ^ (4 * ((lane >> 4) & 3));
+    const int ld_chl = lane >> 4;
+    const uint32_t ld_koff = (uint32_t)((ld_rib * p.k_sn + ld_chl * 8) * 2);
+    const uint32_t ld_voff = (uint32_t)((ld_rib * p.v_sn + ld_chl * 8) * 2);
+
+    const float c = p.c;
+    const int qsign = p.neg ? (int)0x80008000u : 0;
+    const elem* const qg = (const elem*)p.q;
+    const elem* const kg = (const elem*)p.k;
+    const elem* const vgp = (const elem*)p.v;
+    elem* const og = (elem*)p.o;
+
+    int t;
+    if (p.ticket) {
+        if (tid == 0) s_ticket = (int)atomicAdd(p.ticket, 1u);
+        __syncthreads();
+        t = s_ticket;
+    } else {
+        t = blockIdx.x;
+    }
+
+    while (t < p.num_tasks) {
+        int nxt = 0;
+        if (p.ticket && tid == 0) nxt = (int)atomicAdd(p.ticket, 1u);
+
+        int bh, mb;
+        decode_task<CAUSAL>(p, t, bh, mb);
+        const int b = bh / p.H;
+        const int h = bh - b * p.H;
+        const int n = p.n_ctx;
+        const int m0 = mb * BM;
+        const int qrow = m0 + wave * 32 + l32;
+        const int qrow_c = min(qrow, n - 1);
+
+        const elem* qb = qg + b * p.q_sz + h * p.q_sh;
+        const elem* kh = kg + b * p.k_sz + h * p.k_sh;
+        const elem* vh = vgp + b * p.v_sz + h * p.v_sh;
+        elem* ob = og + b * p.o_sz + h * p.o_sh;
+
+        // key tiles of this task
+        const int kv_end = CAUSAL ? min(n, m0 + BM) : n;
+        int j0 = 0, j1 = (kv_end + BN - 1) / BN;
+        if (MODE == MODE_PREFIX) j1 = m0 / BN;
+        if (MODE == MODE_DIAG) j0 = m0 / BN;
+
+        auto load_tile = [&](int j, int buf) {
+            const int kbase = j * BN;
+            const elem* kt0 = kh + (int64_t)kbase * p.k_sn;
+            const elem* vt0 = vh + (int64_t)kbase * p.v_sn;
+            const int last = n - 1 - kbase;  // last row of the tile inside the sequence
+            const bool tail = kbase + BN > n;
+#pragma unroll
+            for (int w0 = 0; w0 < NINST; w0 += NW) {
+                const int w = w0 + wave;
+                if (NINST % NW == 0 || w < NINST) {
+                    const int blk = (w * 64) / (16 * CPR);
+                    const int cg = ((w * 64) % (16 * CPR)) / 64;
+                    const uint32_t dst = smem_addr + buf * BUF + w * 1024;
+                    int row0 = 16 * blk;
+                    uint32_t ko = ld_koff, vo = ld_voff;
+                    if (tail) {
+                        // rows past the sequence re-read its last row (masked later)
+                        const int rb = min(row0, last);
+                        const int rr = min(row0 + ld_rib, last) - rb;
+                        ko = (uint32_t)((rr * p.k_sn + ld_chl * 8) * 2);
+                        vo = (uint32_t)((rr * p.v_sn + ld_chl * 8) * 2);
+                        row0 = rb;
+                    }
+                    const elem* ks = kt0 + (int64_t)row0 * p.k_sn + cg * 32;
+                    const elem* vs = vt0 + (int64_t)row0 * p.v_sn + cg * 32;
+                    if (CPRV == CPR || 4 * cg + ld_chl < CPRV) {
+                        dma16(ks, ko, dst);
+                        dma16(vs, vo, dst + TILE);
+                    }
+                }
+            }
+        };
+
+        if (j0 < j1) load_tile(j0, 0);
+
+        // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
+        // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
+        x8 qf[KST];
+#pragma unroll
+        for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(qb + (int64_t)qrow_c * p.q_sm + (2 * s + hh) * 8);
+#pragma unroll
+        for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+
+        f32x16 o[DT];
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
+        float m_use = -INFINITY;  // running max (exp2 domain) of this lane's query row
+        float l_sum = 0.0f;       // this lane's half of the row sum
+
+        const int srow = bh * p.nmb * BM + m0 + wave * 32 + l32;  // split-state row
+        if (MODE == MODE_DIAG) {
+            // resume from the prefix launch: O holds acc/l in the input dtype
+            const float sm = p.state[srow];
+            const float sl = p.state[(int64_t)p.num_tasks * BM + srow];
+            m_use = sm;
+            l_sum = hh == 0 ? sl : 0.0f;
+            if (qrow < n) {
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) {
+                        const int col = 32 * d + 8 * a + 4 * hh;
+                        if (col < D) {
+                            const x4 v4 = *(const x4*)(ob + (int64_t)qrow * p.o_sm + col);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) o[d][4 * a + e] = (float)v4[e] * sl;
+                        }
+                    }
+            }
+        }
+
+        const int wq_lo = m0 + wave * 32;  // smallest query row of this wave
+        const int wq_hi = wq_lo + 31;      // largest
+        const int lim = CAUSAL ? min(qrow, n - 1) : n - 1;     // last key this lane sees
+        const int vis_lo = CAUSAL ? min(wq_lo, n - 1) : n - 1;  // last key every lane of the wave sees
+        const int vis_hi = CAUSAL ? min(wq_hi, n - 1) : n - 1;  // last key any lane of the wave sees
+
+        // one key tile: S^T, softmax update, O^T += V^T P^T
+        auto tile_step = [&](const RSFA_LDS char* kt_lds, const RSFA_LDS char* vt_lds, int kbase, int nkt_act,
+                             auto masked) {
+            constexpr bool MASK = decltype(masked)::value;
+            f32x16 sacc[NKT];
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < KST; ++s) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+                    if (!MASK || kt < nkt_act) {
+                        const x8 a = *(const RSFA_LDS x8*)(kt_lds + koff[s & 1] + kt * 2 * BLK + s * 512);
+                        sacc[kt] = T::mfma(a, qf[s], sacc[kt]);
+                    }
+                }
+            }
+            if (MASK) {
+                const int rel = lim - kbase - 4 * hh;
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int kk = 32 * kt + 8 * (r >> 2) + (r & 3);
+                        if (kk > rel || kt >= nkt_act) sacc[kt][r] = -INFINITY;
+                    }
+            }
+            float mx = sacc[0][0];
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kt + r > 0) mx = fmaxf(mx, sacc[kt][r]);
+            mx = swap_max(mx);
+            const float m_tile = mx * c;
+            const bool need = m_tile > m_use + RESCALE_SLACK;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float m_new = need ? m_tile : m_use;
+                const float alpha = need ? __builtin_amdgcn_exp2f(m_use - m_new) : 1.0f;
+                l_sum *= alpha;
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+                m_use = m_new;
+            }
+            const float msub = (MASK && m_use == -INFINITY) ? 0.0f : m_use;
+            x8 pk[NKT][2];
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    x2 pr[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i], c, -msub));
+                        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i + 1], c, -msub));
+                        pr[i] = T::cvt2(p0, p1);
+                        l_sum = T::dot2(pr[i], T::ones2(), l_sum);
+                    }
+                    pk[kt][h2] = (x8){pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+#pragma unroll
+                for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2) {
+                        if (!MASK || kt < nkt_act) {
+                            const RSFA_LDS char* vp = vt_lds + (2 * kt + h2) * BLK + d * 1024;
+                            const i32x2 lo = __builtin_bit_cast(i32x2, T::tr_read(vp + voff[0]));
+                            const i32x2 hi = __builtin_bit_cast(i32x2, T::tr_read(vp + voff[1]));
+                            const x8 a = __builtin_bit_cast(x8, (i32x4){lo[0], lo[1], hi[0], hi[1]});
+                            o[d] = T::mfma(a, pk[kt][h2], o[d]);
+                        }
+                    }
+                }
+            }
+        };
+
+        // Key tiles [j0, ju) are visible to every row of this wave (mask-free
+        // body); [ju, j1) straddle the causal diagonal or the sequence end.
+        // Both loops run the same barrier sequence in every wave.
+        int ju = min(j1, (vis_lo + 1) / BN);
+        ju = max(ju, j0);
+        int j = j0;
+        for (; j < ju; ++j) {
+            const int buf = (j - j0) & 1;
+            wait_loads_and_sync();
+            if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
+            const RSFA_LDS char* kl = smem + buf * BUF;
+            tile_step(kl, kl + TILE, j * BN, NKT, std::integral_constant<bool, false>());
+        }
+        for (; j < j1; ++j) {
+            const int buf = (j - j0) & 1;
+            wait_loads_and_sync();
+            if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
+            const int kbase = j * BN;
+            if (kbase <= vis_hi) {
+                const RSFA_LDS char* kl = smem + buf * BUF;
+                const int nkt_act = min(NKT, (vis_hi - kbase) / 32 + 1);
+                tile_step(kl, kl + TILE, kbase, nkt_act, std::integral_constant<bool, true>());
+            }
+        }
+
+        // epilogue
+        const float lt = swap_sum(l_sum);
+        if (MODE == MODE_PREFIX) {
+            if (hh == 0) {
+                p.state[srow] = m_use;
+                p.state[(int64_t)p.num_tasks * BM + srow] = lt;
+            }
+        }
+        const float inv = (MODE == MODE_PREFIX) ? (lt > 0.0f ? 1.0f / lt : 0.0f) : 1.0f / lt;
+        if (qrow < n) {
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const int col = 32 * d + 8 * a + 4 * hh;
+                    if (col < D) {
+                        x4 v4;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v4[e] = (elem)(o[d][4 * a + e] * inv);
+                        *(x4*)(ob + (int64_t)qrow * p.o_sm + col) = v4;
+                    }
+                }
+            if (MODE != MODE_PREFIX && p.lse && hh == 0)
+                p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;
+        }
+
+        if (p.ticket) {
+            __syncthreads();
+            if (tid == 0) s_ticket = nxt;
+            __syncthreads();
+            t = s_ticket;
+        } else {
+            __syncthreads();
+            t += gridDim.x;
+        }
+    }
+
+    // The workgroup holding the last ticket handed out returns the counter to
+    // zero for the next launch on this stream: every workgroup draws exactly one
+    // ticket >= num_tasks, so that ticket is num_tasks + gridDim.x - 1.
+    if (p.ticket && tid == 0 && t == p.num_tasks + (int)gridDim.x - 1) atomicExch(p.ticket, 0u);
+}
+
+}  // namespace rsfa

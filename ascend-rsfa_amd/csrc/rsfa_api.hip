@@ -1,0 +1,375 @@
+// C ABI of the gfx950 FlashAttention-2 forward library (declared in include/rsfa.h).
+//
+// Replaces the host half of the reference operator
+// (ascend_rsfa/flash_attention_forward.py): argument checks of
+// _attention.forward (551-556), the dispatch to the small / causal-split /
+// persistent kernels (564-610), _run_causal_split (493-541), get_tiling
+// (624-665) and get_num_compute_cores (19-21).
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/rsfa.h"
+#include "fa_fwd_kernel.hpp"
+#include "kernel_table.hpp"
+
+namespace rsfa {
+namespace {
+
+constexpr int kMaxDevices = 64;
+constexpr int kTicketSlots = 256;       // concurrent streams with a dynamic queue
+constexpr int kTicketStrideWords = 16;  // one 64-byte line per counter
+constexpr int kLdsPerCu = 160 * 1024;   // gfx950
+
+KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256()};
+
+template <class F>
+void for_each_kernel(F&& f) {
+    for (const KernelList& l : all_lists)
+        for (int i = 0; i < l.count; ++i) f(l.entries[i]);
+}
+
+const KernelEntry* find_kernel(int dtype, int d, int bn, int nw, int causal, int mode) {
+    const KernelEntry* hit = nullptr;
+    for_each_kernel([&](const KernelEntry& e) {
+        if (e.dtype == dtype && e.d == d && e.bn == bn && e.nw == nw && e.causal == causal && e.mode == mode)
+            hit = &e;
+    });
+    return hit;
+}
+
+bool valid_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+struct DeviceState {
+    std::once_flag once;
+    int status = RSFA_OK;
+    int num_cus = 0;
+    uint32_t* tickets = nullptr;  // kTicketSlots counters, each returns to 0 after its launch
+    std::mutex mu;
+    std::unordered_map<void*, int> stream_slot;
+    std::unordered_map<const void*, int> occupancy;  // kernel -> resident workgroups per CU
+};
+
+DeviceState g_dev[kMaxDevices];
+
+int current_device(int* dev) {
+    if (hipGetDevice(dev) != hipSuccess) return RSFA_E_DEVICE;
+    if (*dev < 0 || *dev >= kMaxDevices) return RSFA_E_DEVICE;
+    return RSFA_OK;
+}
+
+DeviceState* device_state(int dev, bool need_tickets, int* status) {
+    DeviceState& ds = g_dev[dev];
+    std::call_once(ds.once, [&] {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            ds.status = RSFA_E_DEVICE;
+            return;
+        }
+        ds.num_cus = cus;
+        void* buf = nullptr;
+        const size_t bytes = sizeof(uint32_t) * kTicketSlots * kTicketStrideWords;
+        if (hipMalloc(&buf, bytes) != hipSuccess || hipMemset(buf, 0, bytes) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess) {
+            ds.status = RSFA_E_DEVICE;
+            return;
+        }
+        ds.tickets = (uint32_t*)buf;
+    });
+    (void)need_tickets;
+    *status = ds.status;
+    return ds.status == RSFA_OK ? &ds : nullptr;
+}
+
+// Counter for launches on `stream`.  Launches on one stream run in order, and
+// each launch leaves its counter at 0 when it ends, so a stream can reuse its
+// counter; distinct streams get distinct counters.  Returns null when all
+// counters are taken (the launch then uses the static schedule).
+uint32_t* stream_ticket(DeviceState& ds, void* stream) {
+    std::lock_guard<std::mutex> lock(ds.mu);
+    auto it = ds.stream_slot.find(stream);
+    int slot;
+    if (it != ds.stream_slot.end()) {
+        slot = it->second;
+    } else {
+        if ((int)ds.stream_slot.size() >= kTicketSlots) return nullptr;
+        slot = (int)ds.stream_slot.size();
+        ds.stream_slot.emplace(stream, slot);
+    }
+    return ds.tickets + (size_t)slot * kTicketStrideWords;
+}
+
+int resident_wgs(DeviceState& ds, const KernelEntry& e) {
+    std::lock_guard<std::mutex> lock(ds.mu);
+    auto it = ds.occupancy.find(e.fn);
+    if (it != ds.occupancy.end()) return it->second;
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, e.fn, e.nw * 64, 0) != hipSuccess || nb <= 0) nb = 1;
+    ds.occupancy.emplace(e.fn, nb);
+    return nb;
+}
+
+// ---------------------------------------------------------------------------
+// Tile search.  The reference's get_tiling is a table of Ascend UB tilings
+// (flash_attention_forward.py:628-664) and its search tool times every
+// (BM, BN) pair (tiling/search_optimal_tiling.py:47-81).  Here the candidates
+// are the compiled instantiations for (dtype, head dim); each is checked
+// against gfx950's per-SIMD register file and per-CU LDS and scored with a
+// cost model: the persistent grid's makespan in key-tile steps, where a step of
+// a BM x BN tile costs its MFMA cycles plus a fixed per-tile synchronisation
+// overhead, and workgroups sharing a CU share its four SIMDs.
+// ---------------------------------------------------------------------------
+struct TileCost {
+    bool feasible;
+    double cycles;
+};
+
+int vgpr_estimate(const KernelEntry& e) {
+    const int dp = e.d < 32 ? 32 : e.d;
+    const int q = (e.d / 16) * 4;        // Q^T fragments
+    const int o = (dp / 32) * 16;        // O^T accumulators
+    const int s = (e.bn / 32) * 16;      // S^T accumulators
+    const int pk = (e.bn / 32) * 8;      // packed P
+    return q + o + s + pk + 40;          // addresses, softmax state, fragments in flight
+}
+
+TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int num_cus) {
+    TileCost tc{false, 0.0};
+    const int dp = e.d < 32 ? 32 : e.d;
+    const int lds = 2 * 2 * e.bn * dp * 2;
+    const int budget = 512 / e.occ;
+    if (vgpr_estimate(e) > budget || lds > kLdsPerCu) return tc;
+    const int wg_by_waves = (4 * e.occ) / e.nw;
+    const int wg_by_lds = kLdsPerCu / lds;
+    const int wg_per_cu = std::max(1, std::min(wg_by_waves, wg_by_lds));
+    const int bm = 32 * e.nw;
+    const int64_t nmb = (n + bm - 1) / bm;
+    const int64_t tiles_full = (n + e.bn - 1) / e.bn;
+    // cycles one workgroup needs per key tile: two GEMMs of 32 x BN x D per wave
+    // at 1024 flop/cycle/SIMD, a wave per SIMD slot, plus sync overhead.
+    const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0 * e.nw / 4.0 * wg_per_cu;
+    const double step = mfma + 220.0;
+    double total = 0.0, longest = 0.0;
+    for (int64_t mb = 0; mb < nmb; ++mb) {
+        const int64_t tiles = e.causal ? std::min<int64_t>(tiles_full, ((mb + 1) * bm + e.bn - 1) / e.bn) : tiles_full;
+        const double c = tiles * step + 600.0;  // + task setup / epilogue
+        total += c;
+        longest = std::max(longest, c);
+    }
+    total *= (double)(z * h);
+    const double slots = (double)num_cus * wg_per_cu;
+    tc.feasible = true;
+    tc.cycles = std::max(total / slots, longest) / wg_per_cu;
+    return tc;
+}
+
+int choose_tiling(int64_t z, int64_t h, int64_t n, int64_t d, int causal, int dtype, int num_cus,
+                  const KernelEntry** out) {
+    const KernelEntry* best = nullptr;
+    double best_cycles = 0.0;
+    for_each_kernel([&](const KernelEntry& e) {
+        if (e.dtype != dtype || e.d != d || e.causal != (causal ? 1 : 0) || e.mode != MODE_FUSED) return;
+        const TileCost tc = tile_cost(e, z, h, n, num_cus);
+        if (!tc.feasible) return;
+        if (!best || tc.cycles < best_cycles - 1e-6 ||
+            (std::fabs(tc.cycles - best_cycles) <= 1e-6 && e.bn > best->bn)) {
+            best = &e;
+            best_cycles = tc.cycles;
+        }
+    });
+    if (!best) return RSFA_E_TILE;
+    *out = best;
+    return RSFA_OK;
+}
+
+int resolve(int64_t d, int causal, int dtype, int req_bm, int req_bn, const KernelEntry** out) {
+    if (!is_pow2(req_bm) || !is_pow2(req_bn) || req_bm < 16 || req_bn < 16 || req_bm > 512 || req_bn > 512 ||
+        (int64_t)req_bm * req_bn > 65536)
+        return RSFA_E_TILE;
+    if (causal && req_bn > req_bm) return RSFA_E_TILE;
+    const KernelEntry* best = nullptr;
+    double best_dist = 0.0;
+    for_each_kernel([&](const KernelEntry& e) {
+        if (e.dtype != dtype || e.d != d || e.causal != (causal ? 1 : 0) || e.mode != MODE_FUSED) return;
+        const double dist = std::fabs(std::log2((double)(32 * e.nw) / req_bm)) + std::fabs(std::log2((double)e.bn / req_bn));
+        if (!best || dist < best_dist - 1e-9 || (std::fabs(dist - best_dist) <= 1e-9 && e.bn > best->bn)) {
+            best = &e;
+            best_dist = dist;
+        }
+    });
+    if (!best) return RSFA_E_TILE;
+    *out = best;
+    return RSFA_OK;
+}
+
+int check_tensor(const void* ptr, const int64_t st[4]) {
+    if (((uintptr_t)ptr & 15) != 0) return RSFA_E_ALIGN;
+    if (st[3] != 1) return RSFA_E_ALIGN;
+    for (int i = 0; i < 3; ++i)
+        if (st[i] < 0 || (st[i] & 7) != 0) return RSFA_E_ALIGN;
+    // per-lane 32-bit byte offsets of the LDS loader cover 16 rows
+    if (st[2] >= (int64_t(1) << 25)) return RSFA_E_ALIGN;
+    return RSFA_OK;
+}
+
+}  // namespace
+}  // namespace rsfa
+
+using namespace rsfa;
+
+extern "C" {
+
+int rsfa_abi_version(void) { return RSFA_ABI_VERSION; }
+
+const char* rsfa_strerror(int status) {
+    switch (status) {
+        case RSFA_OK: return "success";
+        case RSFA_E_NULL: return "a required pointer is NULL";
+        case RSFA_E_SHAPE: return "invalid shape: Z, H and N_CTX must be >= 1 and fit the 32-bit task index";
+        case RSFA_E_HEADDIM: return "head_dim must be one of 16, 32, 64, 128, 256";
+        case RSFA_E_DTYPE: return "dtype must be float16 or bfloat16";
+        case RSFA_E_TILE: return "invalid BLOCK_M/BLOCK_N: powers of two in [16, 512], BLOCK_M*BLOCK_N <= 65536, "
+                                 "and BLOCK_N <= BLOCK_M when causal";
+        case RSFA_E_ALIGN: return "tensors need a unit last-dim stride, other strides multiple of 8 elements "
+                                  "and 16-byte aligned base pointers";
+        case RSFA_E_DEVICE: return "HIP runtime error while preparing the device";
+        case RSFA_E_LAUNCH: return "kernel launch failed";
+        case RSFA_E_ABI: return "rsfa_fwd_args.struct_size does not match this library";
+        case RSFA_E_WORKSPACE: return "causal split mode needs a workspace of rsfa_split_workspace_bytes()";
+        default: return "unknown rsfa status";
+    }
+}
+
+int rsfa_get_num_compute_cores(int device) {
+    int dev = device;
+    if (dev < 0) {
+        const int st = current_device(&dev);
+        if (st != RSFA_OK) return st;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return RSFA_E_DEVICE;
+    return cus;
+}
+
+int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype, int32_t req_block_m, int32_t req_block_n,
+                        int32_t* block_m, int32_t* block_n) {
+    if (!block_m || !block_n) return RSFA_E_NULL;
+    if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
+    if (dtype != RSFA_DTYPE_F16 && dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    const KernelEntry* e = nullptr;
+    const int st = resolve(head_dim, causal, dtype, req_block_m, req_block_n, &e);
+    if (st != RSFA_OK) return st;
+    *block_m = 32 * e->nw;
+    *block_n = e->bn;
+    return RSFA_OK;
+}
+
+int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32_t causal, int32_t dtype,
+                    int32_t* block_m, int32_t* block_n) {
+    if (!block_m || !block_n) return RSFA_E_NULL;
+    if (z < 1 || h < 1 || n_ctx < 1) return RSFA_E_SHAPE;
+    if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
+    if (dtype != RSFA_DTYPE_F16 && dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    // The cost model is evaluated for a 256-CU MI355X so the answer does not
+    // depend on whether a GPU is visible to the caller.
+    const KernelEntry* e = nullptr;
+    const int st = choose_tiling(z, h, n_ctx, head_dim, causal, dtype, 256, &e);
+    if (st != RSFA_OK) return st;
+    *block_m = 32 * e->nw;
+    *block_n = e->bn;
+    return RSFA_OK;
+}
+
+uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32_t block_m) {
+    (void)head_dim;
+    if (z < 1 || h < 1 || n_ctx < 1 || block_m < 1) return 0;
+    const int64_t nmb = (n_ctx + block_m - 1) / block_m;
+    return (uint64_t)(2 * z * h * nmb * block_m) * sizeof(float);
+}
+
+int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
+    if (!a) return RSFA_E_NULL;
+    if (a->struct_size != sizeof(rsfa_fwd_args)) return RSFA_E_ABI;
+    if (!a->q || !a->k || !a->v || !a->o) return RSFA_E_NULL;
+    if (a->dtype != RSFA_DTYPE_F16 && a->dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    if (!valid_head_dim(a->head_dim)) return RSFA_E_HEADDIM;
+    if (a->z < 1 || a->h < 1 || a->n_ctx < 1 || a->n_ctx > (1 << 30) || a->z * a->h > (1 << 30))
+        return RSFA_E_SHAPE;
+    int st;
+    if ((st = check_tensor(a->q, a->q_stride)) != RSFA_OK) return st;
+    if ((st = check_tensor(a->k, a->k_stride)) != RSFA_OK) return st;
+    if ((st = check_tensor(a->v, a->v_stride)) != RSFA_OK) return st;
+    if ((st = check_tensor(a->o, a->o_stride)) != RSFA_OK) return st;
+    if (((uintptr_t)a->lse & 3) != 0) return RSFA_E_ALIGN;
+    const bool causal = a->causal != 0;
+    const bool split = causal && (a->flags & RSFA_FLAG_CAUSAL_SPLIT);
+
+    int dev = 0;
+    if ((st = current_device(&dev)) != RSFA_OK) return st;
+    DeviceState* ds = device_state(dev, true, &st);
+    if (!ds) return st;
+
+    const KernelEntry* e = nullptr;
+    if (a->block_m == 0 && a->block_n == 0)
+        st = choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, ds->num_cus, &e);
+    else
+        st = resolve(a->head_dim, causal, a->dtype, a->block_m, a->block_n, &e);
+    if (st != RSFA_OK) return st;
+    const int bm = 32 * e->nw;
+
+    FwdParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.lse = a->lse;
+    p.q_sz = a->q_stride[0], p.q_sh = a->q_stride[1], p.q_sm = a->q_stride[2];
+    p.k_sz = a->k_stride[0], p.k_sh = a->k_stride[1], p.k_sn = a->k_stride[2];
+    p.v_sz = a->v_stride[0], p.v_sh = a->v_stride[1], p.v_sn = a->v_stride[2];
+    p.o_sz = a->o_stride[0], p.o_sh = a->o_stride[1], p.o_sm = a->o_stride[2];
+    p.H = (int32_t)a->h;
+    p.n_ctx = (int32_t)a->n_ctx;
+    p.nmb = (int32_t)((a->n_ctx + bm - 1) / bm);
+    p.num_heads = (int32_t)(a->z * a->h);
+    if ((int64_t)p.num_heads * p.nmb > (int64_t(1) << 30)) return RSFA_E_SHAPE;
+    p.num_tasks = p.num_heads * p.nmb;
+    const float sc = a->sm_scale;
+    p.c = std::fabs(sc) * 1.4426950408889634f;
+    p.neg = sc < 0.0f ? 1u : 0u;
+
+    if (split) {
+        const uint64_t need = rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm);
+        if (!a->workspace || a->workspace_bytes < need) return RSFA_E_WORKSPACE;
+        if (((uintptr_t)a->workspace & 3) != 0) return RSFA_E_ALIGN;
+        p.state = (float*)a->workspace;
+    }
+
+    const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE);
+    const int modes[2] = {split ? MODE_PREFIX : MODE_FUSED, MODE_DIAG};
+    const int launches = split ? 2 : 1;
+    for (int li = 0; li < launches; ++li) {
+        const KernelEntry* k = find_kernel(a->dtype, (int)a->head_dim, e->bn, e->nw, causal ? 1 : 0, modes[li]);
+        if (!k) return RSFA_E_TILE;
+        const int wgs = resident_wgs(*ds, *k);
+        int64_t grid = (int64_t)ds->num_cus * wgs;
+        grid = std::min<int64_t>(grid, p.num_tasks);
+        grid = std::max<int64_t>(grid, 1);
+        // causal: a heavy-first group spans about one grid's worth of tasks
+        p.group = causal ? (int32_t)std::max<int64_t>(1, std::min<int64_t>(p.num_heads, grid / p.nmb)) : 1;
+        p.ticket = dynamic ? stream_ticket(*ds, stream) : nullptr;
+        void* args[] = {&p};
+        if (hipLaunchKernel(k->fn, dim3((unsigned)grid), dim3((unsigned)(k->nw * 64)), args, 0,
+                            (hipStream_t)stream) != hipSuccess)
+            return RSFA_E_LAUNCH;
+    }
+    return RSFA_OK;
+}
+
+}  // extern "C"

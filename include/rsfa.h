@@ -1,0 +1,134 @@
+/*
+ * rsfa.h - C ABI of the MI355X (gfx950) FlashAttention-2 forward library.
+ *
+ * This is the only native boundary of the package.  The Python module
+ * ascend_rsfa.flash_attention_forward binds it with ctypes; any other host
+ * language can bind the same symbols (plain pointers, sizes and ints, no
+ * torch or C++ types in any signature).
+ *
+ * Every entry point below replaces one piece of the reference operator
+ * (Dell710000/ascend-rsfa, file ascend_rsfa/flash_attention_forward.py):
+ *
+ *   rsfa_attention_fwd        -> _attention.forward, lines 547-616, i.e. the
+ *                                kernel launches at 565, 574, 599 and the causal
+ *                                two-launch split _run_causal_split (493-541)
+ *   rsfa_get_tiling           -> get_tiling(Z, H, N_CTX, HEAD_DIM, causal), 624-665
+ *   rsfa_resolve_tiling       -> the (BLOCK_M, BLOCK_N) meta-parameters the
+ *                                reference passes to _attn_fwd[grid] (518-519, 606-607)
+ *   rsfa_get_num_compute_cores-> get_num_compute_cores(), 19-21
+ *   rsfa_strerror             -> (no counterpart: the reference raises Python
+ *                                exceptions; codes map to them in the wrapper)
+ *
+ * Conventions
+ *   - All tensor pointers are device pointers owned by the caller; the library
+ *     never frees them.  Strides are in elements.  The last (head-dim) stride
+ *     of q/k/v/o must be 1, every other stride a multiple of 8 elements and
+ *     every base pointer 16-byte aligned (RSFA_E_ALIGN otherwise).
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t, NULL = the
+ *     null stream).  The call returns after the launch, not after completion.
+ *   - Return codes: 0 on success, a negative rsfa_status otherwise.  Invalid
+ *     arguments are rejected before anything is launched.
+ */
+#ifndef RSFA_H_
+#define RSFA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RSFA_ABI_VERSION 1
+
+typedef enum rsfa_status {
+    RSFA_OK          = 0,
+    RSFA_E_NULL      = -1,  /* a required pointer is NULL                      */
+    RSFA_E_SHAPE     = -2,  /* Z, H or N_CTX not >= 1, or too large             */
+    RSFA_E_HEADDIM   = -3,  /* head_dim not in {16, 32, 64, 128, 256}           */
+    RSFA_E_DTYPE     = -4,  /* dtype not RSFA_DTYPE_F16 / RSFA_DTYPE_BF16       */
+    RSFA_E_TILE      = -5,  /* block_m/block_n invalid (see rsfa_resolve_tiling)*/
+    RSFA_E_ALIGN     = -6,  /* stride / alignment contract violated             */
+    RSFA_E_DEVICE    = -7,  /* HIP runtime error while querying or preparing    */
+    RSFA_E_LAUNCH    = -8,  /* kernel launch failed                             */
+    RSFA_E_ABI       = -9,  /* struct_size does not match this library          */
+    RSFA_E_WORKSPACE = -10  /* split mode without a large enough workspace      */
+} rsfa_status;
+
+typedef enum rsfa_dtype {
+    RSFA_DTYPE_F16  = 0,
+    RSFA_DTYPE_BF16 = 1
+} rsfa_dtype;
+
+/* flags (bit set) */
+#define RSFA_FLAG_STATIC_SCHEDULE 0x1u /* grid-stride task order instead of the
+                                          dynamic atomic-ticket queue            */
+#define RSFA_FLAG_CAUSAL_SPLIT    0x2u /* causal only: two launches, mask-free
+                                          prefix then masked diagonal, with the
+                                          (m, l, acc) state handed over through
+                                          `workspace` (reference 493-541)       */
+
+typedef struct rsfa_fwd_args {
+    uint32_t    struct_size;  /* = sizeof(rsfa_fwd_args)                        */
+    int32_t     dtype;        /* rsfa_dtype of q, k, v and o                    */
+    const void *q;            /* [Z, H, N_CTX, D]                               */
+    const void *k;            /* [Z, H, N_CTX, D]                               */
+    const void *v;            /* [Z, H, N_CTX, D]                               */
+    void       *o;            /* [Z, H, N_CTX, D], same dtype as q              */
+    float      *lse;          /* optional [Z, H, N_CTX] fp32, natural-log
+                                 logsumexp of the scaled scores (the reference's
+                                 M = m + ln(l), 400-403); NULL = not written    */
+    void       *workspace;    /* split mode only, see rsfa_split_workspace_bytes */
+    uint64_t    workspace_bytes;
+    int64_t     z, h, n_ctx, head_dim;
+    int64_t     q_stride[4];  /* element strides of dims (Z, H, N_CTX, D)       */
+    int64_t     k_stride[4];
+    int64_t     v_stride[4];
+    int64_t     o_stride[4];
+    float       sm_scale;     /* multiplies q.k before the softmax              */
+    int32_t     causal;       /* 0/1: key n visible to query m iff n <= m       */
+    int32_t     block_m;      /* requested BLOCK_M, 0 = choose (rsfa_get_tiling)*/
+    int32_t     block_n;      /* requested BLOCK_N, 0 = choose                  */
+    uint32_t    flags;        /* RSFA_FLAG_*                                    */
+} rsfa_fwd_args;
+
+/* Fused FlashAttention-2 forward: o = softmax(q k^T * sm_scale [+ causal mask]) v.
+ * Replaces _attention.forward (flash_attention_forward.py:547-616). */
+int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
+
+/* Bytes of fp32 workspace RSFA_FLAG_CAUSAL_SPLIT needs for this problem and
+ * tiling (the reference allocates state[2, Z, H, NBM, BM] at 501; this library
+ * also keeps the un-normalised accumulator in fp32 instead of fp16 in O). */
+uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
+                                    int64_t head_dim, int32_t block_m);
+
+/* Tile search for gfx950 (replaces the lookup table get_tiling, 624-665):
+ * writes the (BLOCK_M, BLOCK_N) this library would pick for the shape.
+ * Never fails for a valid shape. */
+int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim,
+                    int32_t causal, int32_t dtype, int32_t *block_m,
+                    int32_t *block_n);
+
+/* Maps a caller-requested (BLOCK_M, BLOCK_N) to the compiled instantiation
+ * that runs it.  Requests follow the reference's rules (powers of two,
+ * 16 <= BLOCK <= 512, BLOCK_M*BLOCK_N <= 65536, causal needs
+ * BLOCK_N <= BLOCK_M, which the reference silently breaks on, see
+ * benchmarks/run_correctness_test.py:24-25).  Returns RSFA_E_TILE otherwise. */
+int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype,
+                        int32_t req_block_m, int32_t req_block_n,
+                        int32_t *block_m, int32_t *block_n);
+
+/* Number of compute units of `device` (-1 = current device); replaces
+ * get_num_compute_cores (19-21).  Negative rsfa_status on error. */
+int rsfa_get_num_compute_cores(int device);
+
+/* Static string for a status code. */
+const char *rsfa_strerror(int status);
+
+/* RSFA_ABI_VERSION the library was built with. */
+int rsfa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RSFA_H_ */
