@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cfloat>
 #include <cmath>
 #include <mutex>
 #include <unordered_map>
@@ -342,6 +343,11 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     p.num_tasks = p.num_heads * p.nmb;
     const float sc = a->sm_scale;
     p.c = std::fabs(sc) * 1.4426950408889634f;
+    // Masked scores are -inf and the kernel forms exp2(s * c - m): with c == 0
+    // that is -inf * 0 = NaN.  FLT_MIN scales every finite fp16/bf16 score
+    // product (|s| < 2^40) below 2^-86, so exp2 of it is exactly 1.0f, the
+    // value sm_scale == 0 gives, while masked keys still get exp2(-inf) = 0.
+    if (p.c < FLT_MIN) p.c = FLT_MIN;
     p.neg = sc < 0.0f ? 1u : 0u;
 
     if (split) {
