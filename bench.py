@@ -1,13 +1,21 @@
 """Benchmark of the FlashAttention-2 forward on one MI355X.
 
 Prints ONE JSON line.  A step is one ``attention(q, k, v, causal, sm_scale,
-BM, BN)`` call over the workload's synthetic, HBM-resident Q/K/V; ``value`` is
-the algorithmic throughput 4*B*H*S^2*D (x0.5 causal) / time in TFLOP/s for the
-BASELINE workload configs[1] (non-causal B=32 H=8 S=2048 D=128).  The other
-BASELINE configs and the north-star target shape are timed too and reported
-under ``"configs"``.
+BM, BN)`` call (the reference's public entry point) over the workload's
+seeded synthetic Q/K/V, already resident in HBM.  ``value`` is the algorithmic
+throughput 4*B*H*S^2*D (x0.5 causal) / time in TFLOP/s of the BASELINE workload
+configs[1] (non-causal B=32 H=8 S=2048 D=128), timed as K back-to-back calls
+between two HIP events on the stream the kernel is launched on.  The other
+BASELINE configs and the north-star target shape are timed the same way and
+reported under ``"configs"``.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
+                    [--calibrate-copy-mib M]
+
+``--calibrate-copy-mib M`` adds one plain device-to-device copy of M MiB after
+the timed work; under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives
+the counter reading of a kernel with known traffic, which scales the readings
+of the attention kernel to bytes.
 """
 import argparse
 import json
@@ -34,15 +42,18 @@ CONFIGS = [
     ("C5", 4, 16, 8192, 64, True, 1 / 8, 1239),
     ("C1", 2, 8, 1024, 128, True, 0.5, 1235),
 ]
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "traffic_fa_fwd_c2.json")
+# HBM bytes per launch of the C2 kernel, from two rocprofv3 --pmc passes
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "fa_fwd_c2_traffic.txt")
 
 
 def flops(B, H, S, D, causal):
     return 4.0 * B * H * S * S * D * (0.5 if causal else 1.0)
 
 
-def algo_bytes(B, H, S, D):
-    return 2.0 * 4 * B * H * S * D  # Q, K, V read once, O written once (fp16)
+def algo_bytes(B, H, S, D, causal):
+    # Q, K, V read once, O written once (fp16); non-causal attention() also
+    # writes the fp32 row logsumexp M (reference flash_attention_forward.py:400-403)
+    return 2.0 * 4 * B * H * S * D + (0.0 if causal else 4.0 * B * H * S)
 
 
 def time_config(F, torch, cfg, steps, warmup):
@@ -56,43 +67,46 @@ def time_config(F, torch, cfg, steps, warmup):
     BM, BN = F.get_tiling(B, H, S, D, causal)
     for _ in range(warmup):
         F.attention(q, k, v, causal, scale, BM, BN)
-    torch.cuda.synchronize()
+    # attention() enqueues its kernel on the current stream: the events go there
     stream = torch.cuda.current_stream()
-    # whole-job timing: K back-to-back calls between two events
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0.record(stream)
     for _ in range(steps):
         F.attention(q, k, v, causal, scale, BM, BN)
     t1.record(stream)
     torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    # per-launch kernel duration, events on the stream the kernel runs on
-    per = []
-    for _ in range(min(steps, 10)):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        F.forward(q, k, v, causal, scale, BM, BN)  # kernel only (no LSE / autograd wrapper)
-        e1.record(stream)
-        per.append((e0, e1))
-    torch.cuda.synchronize()
-    kern_ms = sorted(a.elapsed_time(b) for a, b in per)
-    kern_ms = kern_ms[len(kern_ms) // 2]
+    ms = t0.elapsed_time(t1) / steps
     fl = flops(B, H, S, D, causal)
-    ms = total_ms / steps
     del q, k, v
     torch.cuda.empty_cache()
     return {
         "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "tiling": [BM, BN],
         "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
         "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
-        "kernel_ms": round(kern_ms, 4), "kernel_tflops": round(fl / (kern_ms * 1e-3) / 1e12, 1),
+        "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal) / (ms * 1e-3) / 1e9, 1),
     }
 
 
-def cpu_baseline(torch, cfg, budget_s=12.0):
-    """The reference's attention math (oracle closed form, fp32) on host cores, bounded sample."""
+def calibrate_copy(torch, mib):
+    """One plain device copy of `mib` MiB (reads and writes mib MiB each)."""
+    n = mib * (1 << 20)
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(torch, cfg, budget_s=10.0):
+    """The reference's attention math (the oracle's fp32 closed form) on the host cores.
+
+    Bounded sample: whole heads of the workload, repeated until about
+    ``budget_s`` seconds of CPU time have run.
+    """
     from oracle import attention as oracle
 
     name, B, H, S, D, causal, scale, seed = cfg
@@ -104,15 +118,20 @@ def cpu_baseline(torch, cfg, budget_s=12.0):
     one = max(time.perf_counter() - t, 1e-4)
     heads = max(1, min(B * H, int(budget_s / one)))
     q, k, v = oracle.make_inputs(1, heads, S, D, seed)
+    reps = 0
     t = time.perf_counter()
-    oracle.reference_attention(q, k, v, causal, scale)
-    el = time.perf_counter() - t
-    fl = flops(1, heads, S, D, causal)
+    while True:
+        oracle.reference_attention(q, k, v, causal, scale)
+        reps += 1
+        el = time.perf_counter() - t
+        if el >= budget_s * 0.5 or reps >= 20:
+            break
+    fl = flops(1, heads, S, D, causal) * reps
     return {
         "value": round(fl / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": f"{heads} of {B * H} heads of {name} (S={S}, D={D}, causal={causal}), fp32 closed form "
-                  f"softmax(QK^T*scale)V in PyTorch on the host CPU (full S^2 even when causal), "
-                  f"{el:.2f} s; extrapolated full-config time {el * B * H / heads * 1e3:.0f} ms",
+        "sample": f"{reps} x {heads} of {B * H} heads of {name} (S={S}, D={D}, causal={causal}): the fp32 closed "
+                  f"form softmax(QK^T*scale)V in PyTorch on {threads} host threads, {el:.1f} s; "
+                  f"full S^2 computed even when causal; FLOPs counted as on the GPU",
     }
 
 
@@ -123,10 +142,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="time only this config name")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the path shards by (batch, head) with no "
-                                   "communication (see DESIGN.md), so --gpus N>1 is not run"}))
+        print(json.dumps({"error": "this build runs on one GPU only: the path shards by (batch, head) with no "
+                                   "communication, so runs with --gpus N > 1 are not part of it"}))
         sys.exit(2)
 
     import torch
@@ -135,24 +155,26 @@ def main():
     from ascend_rsfa import flash_attention_forward as F
 
     if not os.path.exists(_native.library_path()):
-        import __graft_entry__
-
-        __graft_entry__.build()
+        raise SystemExit(f"{_native.library_path()} is not built: run `python __graft_entry__.py build` first")
     torch.cuda.set_device(0)
     configs = [c for c in CONFIGS if args.only in (None, c[0])]
     results = {}
     for cfg in configs:
         results[cfg[0]] = time_config(F, torch, cfg, args.steps, args.warmup)
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
+    if args.calibrate_copy_mib:
+        calibrate_copy(torch, args.calibrate_copy_mib)
     main_name = configs[0][0]
     r = results[main_name]
     cfg = configs[0]
-    kern_s = r["kernel_ms"] * 1e-3
-    achieved = flops(cfg[1], cfg[2], cfg[3], cfg[4], cfg[5]) / kern_s / 1e12
+    # average duration of one launch over the timed region (back-to-back launches)
+    achieved = flops(*cfg[1:6]) / (r["ms_per_call"] * 1e-3) / 1e12
     traffic = None
-    if os.path.exists(PROFILE_TRAFFIC) and main_name == "C2":
+    if main_name == "C2" and os.path.exists(PROFILE_TRAFFIC):
         with open(PROFILE_TRAFFIC) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(float(line.split(":", 1)[1]))
     line = {
         "metric": METRIC,
         "value": r["tflops"],
