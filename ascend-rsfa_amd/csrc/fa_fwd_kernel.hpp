@@ -45,6 +45,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 namespace rsfa {
 
@@ -174,6 +175,62 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff_bytes, ui
                  :
                  : "v"(voff_bytes), "s"(sbase), "{m0}"(lds_addr)
                  : "memory");
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1.
+template <int... I, class F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(std::make_integer_sequence<int, N>(), f);
+}
+
+// MFMA operands read from LDS ahead of use.  The compiler's scheduler places
+// each LDS read right before its MFMA and waits for it, exposing the LDS
+// latency once per MFMA; here the reads are issued PF MFMAs ahead from inline
+// asm and each MFMA first waits (s_waitcnt lgkmcnt) for its own operand only.
+// The wait takes the operand as an in/out register so the MFMA that consumes
+// it cannot be scheduled before the wait.  LDS operations complete in order,
+// so a wait for "at most N outstanding" (N = reads issued after the one needed)
+// is exact for these reads and only conservative for any LDS or scalar-memory
+// operation the compiler interleaves.
+#ifndef RSFA_QK_PREFETCH
+#define RSFA_QK_PREFETCH 4
+#endif
+#ifndef RSFA_PV_PREFETCH
+#define RSFA_PV_PREFETCH 4
+#endif
+constexpr int QK_PREFETCH = RSFA_QK_PREFETCH;
+constexpr int PV_PREFETCH = RSFA_PV_PREFETCH;
+
+template <int OFF>
+__device__ __forceinline__ i32x4 lds_read_b128(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "DS offset is 16 bits");
+    i32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr16(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "DS offset is 16 bits");
+    i32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+template <int N, class V>
+__device__ __forceinline__ void lgkm_wait(V& v) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+template <int N, class V>
+__device__ __forceinline__ void lgkm_wait2(V& a, V& b) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
 }
 
 __device__ __forceinline__ void wait_loads_and_sync() {
@@ -360,21 +417,45 @@ fa_fwd_kernel(FwdParams p) {
         const int vis_hi = CAUSAL ? min(wq_hi, n - 1) : n - 1;  // last key any lane of the wave sees
 
         // one key tile: S^T, softmax update, O^T += V^T P^T
-        auto tile_step = [&](const RSFA_LDS char* kt_lds, const RSFA_LDS char* vt_lds, int kbase, int nkt_act,
-                             auto masked) {
+        auto tile_step = [&](int buf, int kbase, int nkt_act, auto masked) {
             constexpr bool MASK = decltype(masked)::value;
+            const RSFA_LDS char* kt_lds = smem + buf * BUF;
+            const RSFA_LDS char* vt_lds = kt_lds + TILE;
             f32x16 sacc[NKT];
+            const f32x16 zero = {};  // the first k-step adds to an inline-constant 0
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt)
+            for (int kt = 0; kt < NKT; ++kt) sacc[kt] = zero;
+            if (!MASK) {
+                // MFMA i = (k-step s, sub-tile kt), i = s*NKT + kt; operand ring of PF+1
+                constexpr int NM = KST * NKT;
+                constexpr int PF = QK_PREFETCH < NM ? QK_PREFETCH : NM;
+                constexpr int NB = PF + 1;
+                const uint32_t kb0 = smem_addr + buf * BUF + koff[0];
+                const uint32_t kb1 = smem_addr + buf * BUF + koff[1];
+                i32x4 ring[NB];
+                auto issue = [&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int ss = i / NKT, kt = i % NKT;
+                    ring[i % NB] = lds_read_b128<kt * 2 * BLK + ss * 512>((ss & 1) ? kb1 : kb0);
+                };
+                static_for<PF>(issue);
+                static_for<NM>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int ss = i / NKT, kt = i % NKT;
+                    constexpr int ahead = (NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1);
+                    lgkm_wait<ahead>(ring[i % NB]);
+                    sacc[kt] = T::mfma(__builtin_bit_cast(x8, ring[i % NB]), qf[ss], ss == 0 ? zero : sacc[kt]);
+                    if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
+                });
+            } else {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.0f;
+                for (int s = 0; s < KST; ++s) {
 #pragma unroll
-            for (int s = 0; s < KST; ++s) {
-#pragma unroll
-                for (int kt = 0; kt < NKT; ++kt) {
-                    if (!MASK || kt < nkt_act) {
-                        const x8 a = *(const RSFA_LDS x8*)(kt_lds + koff[s & 1] + kt * 2 * BLK + s * 512);
-                        sacc[kt] = T::mfma(a, qf[s], sacc[kt]);
+                    for (int kt = 0; kt < NKT; ++kt) {
+                        if (kt < nkt_act) {
+                            const x8 a = *(const RSFA_LDS x8*)(kt_lds + koff[s & 1] + kt * 2 * BLK + s * 512);
+                            sacc[kt] = T::mfma(a, qf[s], s == 0 ? zero : sacc[kt]);
+                        }
                     }
                 }
             }
@@ -424,13 +505,41 @@ fa_fwd_kernel(FwdParams p) {
                     pk[kt][h2] = (x8){pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
                 }
             }
+            if (!MASK) {
+                // MFMA i = (d, kt, h2), i = (d*NKT + kt)*2 + h2, two transposing reads each
+                constexpr int NM = DT * NKT * 2;
+                constexpr int PF = PV_PREFETCH < NM ? PV_PREFETCH : NM;
+                constexpr int NB = PF + 1;
+                const uint32_t vb0 = smem_addr + buf * BUF + TILE + voff[0];
+                const uint32_t vb1 = smem_addr + buf * BUF + TILE + voff[1];
+                // the two halves stay separate registers until their wait: a
+                // copy into one 4-register operand before it would read them early
+                i32x2 rlo[NB], rhi[NB];
+                auto issue = [&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int d = i / (2 * NKT), kt = (i / 2) % NKT, h2 = i % 2;
+                    constexpr int off = (2 * kt + h2) * BLK + d * 1024;
+                    rlo[i % NB] = lds_read_tr16<off>(vb0);
+                    rhi[i % NB] = lds_read_tr16<off>(vb1);
+                };
+                static_for<PF>(issue);
+                static_for<NM>([&](auto ic) {
+                    constexpr int i = decltype(ic)::value;
+                    constexpr int d = i / (2 * NKT), kt = (i / 2) % NKT, h2 = i % 2;
+                    constexpr int ahead = 2 * ((NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1));
+                    lgkm_wait2<ahead>(rlo[i % NB], rhi[i % NB]);
+                    const i32x2 lo = rlo[i % NB], hi = rhi[i % NB];
+                    o[d] = T::mfma(__builtin_bit_cast(x8, (i32x4){lo[0], lo[1], hi[0], hi[1]}), pk[kt][h2], o[d]);
+                    if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
+                });
+            } else {
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt) {
 #pragma unroll
                     for (int h2 = 0; h2 < 2; ++h2) {
-                        if (!MASK || kt < nkt_act) {
+                        if (kt < nkt_act) {
                             const RSFA_LDS char* vp = vt_lds + (2 * kt + h2) * BLK + d * 1024;
                             const i32x2 lo = __builtin_bit_cast(i32x2, T::tr_read(vp + voff[0]));
                             const i32x2 hi = __builtin_bit_cast(i32x2, T::tr_read(vp + voff[1]));
@@ -439,6 +548,7 @@ fa_fwd_kernel(FwdParams p) {
                         }
                     }
                 }
+            }
             }
         };
 
@@ -452,8 +562,7 @@ fa_fwd_kernel(FwdParams p) {
             const int buf = (j - j0) & 1;
             wait_loads_and_sync();
             if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
-            const RSFA_LDS char* kl = smem + buf * BUF;
-            tile_step(kl, kl + TILE, j * BN, NKT, std::integral_constant<bool, false>());
+            tile_step(buf, j * BN, NKT, std::integral_constant<bool, false>());
         }
         for (; j < j1; ++j) {
             const int buf = (j - j0) & 1;
@@ -461,9 +570,8 @@ fa_fwd_kernel(FwdParams p) {
             if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
             const int kbase = j * BN;
             if (kbase <= vis_hi) {
-                const RSFA_LDS char* kl = smem + buf * BUF;
                 const int nkt_act = min(NKT, (vis_hi - kbase) / 32 + 1);
-                tile_step(kl, kl + TILE, kbase, nkt_act, std::integral_constant<bool, true>());
+                tile_step(buf, kbase, nkt_act, std::integral_constant<bool, true>());
             }
         }
 
