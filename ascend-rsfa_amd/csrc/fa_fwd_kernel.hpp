@@ -126,11 +126,38 @@ struct FwdParams {
     int32_t nmb;        // query blocks per head = ceil(n_ctx / BM)
     int32_t num_heads;  // Z * H
     int32_t num_tasks;  // num_heads * nmb
-    int32_t group;      // causal: heads per heavy-first group
+    int32_t nq;         // task queues (1 or 8): queue x holds the heads bh % nq == x
     float c;            // |sm_scale| * log2(e)
     uint32_t neg;       // 1 when sm_scale < 0: q is negated (exact) and c = |c|
-    uint32_t* ticket;   // dynamic queue counter (returns to 0 at kernel end) or null
+    uint32_t* ticket;   // dynamic queue counters (nq of them, 16 words apart; each returns
+                        // to 0 at kernel end) or null for the static schedule
 };
+
+// Queues.  Workgroups are dispatched to the 8 XCDs of an MI355X round robin,
+// so workgroup b runs on XCD b % 8 and serves queue b % nq: with nq = 8 all
+// query blocks of a head run on one XCD and its K/V are fetched into that
+// XCD's L2 once, instead of once per XCD.
+struct Queue {
+    int x;      // queue index
+    int nh;     // heads in the queue
+    int ntask;  // tasks in the queue = nh * nmb
+    int nwg;    // workgroups serving the queue
+    int rank;   // this workgroup's rank among them
+    int group;  // causal: heads per heavy-first group
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ Queue make_queue(const FwdParams& p) {
+    Queue q;
+    q.x = (int)blockIdx.x % p.nq;
+    q.rank = (int)blockIdx.x / p.nq;
+    q.nwg = ((int)gridDim.x - q.x + p.nq - 1) / p.nq;
+    q.nh = (p.num_heads - q.x + p.nq - 1) / p.nq;
+    q.ntask = q.nh * p.nmb;
+    // a heavy-first group spans about one round of the queue's workgroups
+    q.group = CAUSAL ? max(1, min(q.nh, q.nwg / p.nmb)) : 1;
+    return q;
+}
 
 __device__ __forceinline__ float swap_max(float x) {
     // {x[l%32], x[l%32 + 32]} in some order for every lane l
@@ -143,25 +170,27 @@ __device__ __forceinline__ float swap_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Task order.  Non-causal: head-major, so consecutive tickets share K/V in L2.
-// Causal: heads in groups of p.group, inside a group the heaviest query blocks
+// Task order inside a queue.  Non-causal: head-major, so consecutive tickets
+// share K/V in L2.  Causal: heads in groups of q.group, inside a group the heaviest query blocks
 // first (longest-processing-time first), which bounds the tail of the
 // persistent grid while keeping a group's K/V resident.
 template <bool CAUSAL>
-__device__ __forceinline__ void decode_task(const FwdParams& p, int t, int& bh, int& mb) {
+__device__ __forceinline__ void decode_task(const FwdParams& p, const Queue& q, int t, int& bh, int& mb) {
+    int lh;  // head index inside the queue
     if (!CAUSAL) {
-        bh = t / p.nmb;
-        mb = t - bh * p.nmb;
+        lh = t / p.nmb;
+        mb = t - lh * p.nmb;
     } else {
-        const int per_group = p.group * p.nmb;
+        const int per_group = q.group * p.nmb;
         const int g = t / per_group;
         const int w = t - g * per_group;
-        const int g0 = g * p.group;
-        const int gc = min(p.group, p.num_heads - g0);
+        const int g0 = g * q.group;
+        const int gc = min(q.group, q.nh - g0);
         const int i = w / gc;
         mb = p.nmb - 1 - i;
-        bh = g0 + (w - i * gc);
+        lh = g0 + (w - i * gc);
     }
+    bh = lh * p.nq + q.x;
 }
 
 // One wave's direct global->LDS load: each lane fetches 16 bytes from
@@ -304,21 +333,23 @@ fa_fwd_kernel(FwdParams p) {
     const elem* const vgp = (const elem*)p.v;
     elem* const og = (elem*)p.o;
 
+    const Queue qu = make_queue<CAUSAL>(p);
+    uint32_t* const ctr = p.ticket ? p.ticket + 16 * qu.x : nullptr;
     int t;
-    if (p.ticket) {
-        if (tid == 0) s_ticket = (int)atomicAdd(p.ticket, 1u);
+    if (ctr) {
+        if (tid == 0) s_ticket = (int)atomicAdd(ctr, 1u);
         __syncthreads();
         t = s_ticket;
     } else {
-        t = blockIdx.x;
+        t = qu.rank;
     }
 
-    while (t < p.num_tasks) {
+    while (t < qu.ntask) {
         int nxt = 0;
-        if (p.ticket && tid == 0) nxt = (int)atomicAdd(p.ticket, 1u);
+        if (ctr && tid == 0) nxt = (int)atomicAdd(ctr, 1u);
 
         int bh, mb;
-        decode_task<CAUSAL>(p, t, bh, mb);
+        decode_task<CAUSAL>(p, qu, t, bh, mb);
         const int b = bh / p.H;
         const int h = bh - b * p.H;
         const int n = p.n_ctx;
@@ -601,21 +632,22 @@ fa_fwd_kernel(FwdParams p) {
                 p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;
         }
 
-        if (p.ticket) {
+        if (ctr) {
             __syncthreads();
             if (tid == 0) s_ticket = nxt;
             __syncthreads();
             t = s_ticket;
         } else {
             __syncthreads();
-            t += gridDim.x;
+            t += qu.nwg;
         }
     }
 
-    // The workgroup holding the last ticket handed out returns the counter to
-    // zero for the next launch on this stream: every workgroup draws exactly one
-    // ticket >= num_tasks, so that ticket is num_tasks + gridDim.x - 1.
-    if (p.ticket && tid == 0 && t == p.num_tasks + (int)gridDim.x - 1) atomicExch(p.ticket, 0u);
+    // The workgroup holding the last ticket handed out by its queue returns the
+    // counter to zero for the next launch on this stream: every workgroup of
+    // the queue draws exactly one ticket >= ntask, so that ticket is
+    // ntask + nwg - 1.
+    if (ctr && tid == 0 && t == qu.ntask + qu.nwg - 1) atomicExch(ctr, 0u);
 }
 
 }  // namespace rsfa

@@ -25,7 +25,9 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 constexpr int kTicketSlots = 256;       // concurrent streams with a dynamic queue
+constexpr int kQueues = 8;              // task queues per launch (one per XCD)
 constexpr int kTicketStrideWords = 16;  // one 64-byte line per counter
+constexpr int kSlotWords = kQueues * kTicketStrideWords;
 constexpr int kLdsPerCu = 160 * 1024;   // gfx950
 
 KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256()};
@@ -76,7 +78,7 @@ DeviceState* device_state(int dev, bool need_tickets, int* status) {
         }
         ds.num_cus = cus;
         void* buf = nullptr;
-        const size_t bytes = sizeof(uint32_t) * kTicketSlots * kTicketStrideWords;
+        const size_t bytes = sizeof(uint32_t) * kTicketSlots * kSlotWords;
         if (hipMalloc(&buf, bytes) != hipSuccess || hipMemset(buf, 0, bytes) != hipSuccess ||
             hipDeviceSynchronize() != hipSuccess) {
             ds.status = RSFA_E_DEVICE;
@@ -104,7 +106,16 @@ uint32_t* stream_ticket(DeviceState& ds, void* stream) {
         slot = (int)ds.stream_slot.size();
         ds.stream_slot.emplace(stream, slot);
     }
-    return ds.tickets + (size_t)slot * kTicketStrideWords;
+    return ds.tickets + (size_t)slot * kSlotWords;
+}
+
+// Task queues of a launch: one per XCD (8) when every queue gets whole heads
+// in near-equal numbers, else a single queue.  The kernel's queue x holds the
+// heads bh % nq == x and is served by workgroups b % nq == x.
+int32_t queue_count(int64_t num_heads, int64_t grid) {
+    if (grid < kQueues || num_heads < kQueues) return 1;
+    if (num_heads % kQueues != 0 && num_heads < 8 * kQueues) return 1;
+    return kQueues;
 }
 
 int resident_wgs(DeviceState& ds, const KernelEntry& e) {
@@ -367,8 +378,7 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
         int64_t grid = (int64_t)ds->num_cus * wgs;
         grid = std::min<int64_t>(grid, p.num_tasks);
         grid = std::max<int64_t>(grid, 1);
-        // causal: a heavy-first group spans about one grid's worth of tasks
-        p.group = causal ? (int32_t)std::max<int64_t>(1, std::min<int64_t>(p.num_heads, grid / p.nmb)) : 1;
+        p.nq = queue_count(p.num_heads, grid);
         p.ticket = dynamic ? stream_ticket(*ds, stream) : nullptr;
         void* args[] = {&p};
         if (hipLaunchKernel(k->fn, dim3((unsigned)grid), dim3((unsigned)(k->nw * 64)), args, 0,
