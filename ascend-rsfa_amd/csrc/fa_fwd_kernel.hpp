@@ -199,8 +199,14 @@ __device__ __forceinline__ void decode_task(const FwdParams& p, const Queue& q, 
 // inline asm so the compiler does not make later LDS reads wait for it; the
 // kernel itself waits (vmcnt(0) + barrier) before reading a buffer a load
 // targets, and only ever loads into the buffer nobody is reading.
+// The compiler's hazard recognizer does not see this asm as a vector-memory
+// instruction, so it adds no wait states for its scalar operands: when the
+// SGPR base was just written by a VALU instruction (e.g. a v_readlane reload of
+// a spilled SGPR), the load would read the stale base.  s_nop 4 supplies the 5
+// wait states "VALU writes SGPR -> VMEM reads that SGPR" needs (and covers the
+// one "write M0 -> LDS DMA" needs).
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff_bytes, uint32_t lds_addr) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
                  : "v"(voff_bytes), "s"(sbase), "{m0}"(lds_addr)
                  : "memory");
@@ -268,7 +274,7 @@ __device__ __forceinline__ void wait_loads_and_sync() {
 }
 
 template <class T, int D, int BN, int NW, bool CAUSAL, int MODE, int OCC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 fa_fwd_kernel(FwdParams p) {
     typedef typename T::elem elem;
     typedef typename T::x8 x8;
@@ -323,8 +329,18 @@ fa_fwd_kernel(FwdParams p) {
     // is the same for every slice.
     const int ld_rib = l16 ^ (4 * ((lane >> 4) & 3));
     const int ld_chl = lane >> 4;
-    const uint32_t ld_koff = (uint32_t)((ld_rib * p.k_sn + ld_chl * 8) * 2);
-    const uint32_t ld_voff = (uint32_t)((ld_rib * p.v_sn + ld_chl * 8) * 2);
+    // Byte offsets of this wave's slices (slice w = sl*NW + wave) from the first
+    // row of a whole tile, for K and V; the tile loop only adds a uniform base.
+    constexpr int NSL = (NINST + NW - 1) / NW;
+    uint32_t kgo[NSL], vgo[NSL];
+#pragma unroll
+    for (int sl = 0; sl < NSL; ++sl) {
+        const int w = sl * NW + wave;
+        const int blk = (w * 64) / (16 * CPR);
+        const int cg = ((w * 64) % (16 * CPR)) / 64;
+        kgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.k_sn + cg * 32 + ld_chl * 8) * 2);
+        vgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.v_sn + cg * 32 + ld_chl * 8) * 2);
+    }
 
     const float c = p.c;
     const int qsign = p.neg ? (int)0x80008000u : 0;
@@ -372,30 +388,39 @@ fa_fwd_kernel(FwdParams p) {
             const int kbase = j * BN;
             const elem* kt0 = kh + (int64_t)kbase * p.k_sn;
             const elem* vt0 = vh + (int64_t)kbase * p.v_sn;
-            const int last = n - 1 - kbase;  // last row of the tile inside the sequence
-            const bool tail = kbase + BN > n;
+            const uint32_t dst0 = smem_addr + buf * BUF;
+            if (kbase + BN <= n) {
+                // whole tile: one uniform base per tensor, per-slice offsets precomputed
 #pragma unroll
-            for (int w0 = 0; w0 < NINST; w0 += NW) {
-                const int w = w0 + wave;
+                for (int sl = 0; sl < NSL; ++sl) {
+                    const int w = sl * NW + wave;
+                    if (NINST % NW == 0 || w < NINST) {
+                        const int cg = ((w * 64) % (16 * CPR)) / 64;
+                        if (CPRV == CPR || 4 * cg + ld_chl < CPRV) {
+                            dma16(kt0, kgo[sl], dst0 + w * 1024);
+                            dma16(vt0, vgo[sl], dst0 + w * 1024 + TILE);
+                        }
+                    }
+                }
+                return;
+            }
+            const int last = n - 1 - kbase;  // last row of the tile inside the sequence
+#pragma unroll
+            for (int sl = 0; sl < NSL; ++sl) {
+                const int w = sl * NW + wave;
                 if (NINST % NW == 0 || w < NINST) {
                     const int blk = (w * 64) / (16 * CPR);
                     const int cg = ((w * 64) % (16 * CPR)) / 64;
-                    const uint32_t dst = smem_addr + buf * BUF + w * 1024;
-                    int row0 = 16 * blk;
-                    uint32_t ko = ld_koff, vo = ld_voff;
-                    if (tail) {
-                        // rows past the sequence re-read its last row (masked later)
-                        const int rb = min(row0, last);
-                        const int rr = min(row0 + ld_rib, last) - rb;
-                        ko = (uint32_t)((rr * p.k_sn + ld_chl * 8) * 2);
-                        vo = (uint32_t)((rr * p.v_sn + ld_chl * 8) * 2);
-                        row0 = rb;
-                    }
+                    // rows past the sequence re-read its last row (masked later)
+                    const int row0 = min(16 * blk, last);
+                    const int rr = min(16 * blk + ld_rib, last) - row0;
+                    const uint32_t ko = (uint32_t)((rr * p.k_sn + ld_chl * 8) * 2);
+                    const uint32_t vo = (uint32_t)((rr * p.v_sn + ld_chl * 8) * 2);
                     const elem* ks = kt0 + (int64_t)row0 * p.k_sn + cg * 32;
                     const elem* vs = vt0 + (int64_t)row0 * p.v_sn + cg * 32;
                     if (CPRV == CPR || 4 * cg + ld_chl < CPRV) {
-                        dma16(ks, ko, dst);
-                        dma16(vs, vo, dst + TILE);
+                        dma16(ks, ko, dst0 + w * 1024);
+                        dma16(vs, vo, dst0 + w * 1024 + TILE);
                     }
                 }
             }

@@ -4,5 +4,9 @@
 
 using namespace rsfa;
 
-RSFA_DEFINE_KERNEL_LIST(kernels_d256,
-    RSFA_TILE_ENTRIES(TypeF16, 0, 256, 32, 4, 2), RSFA_TILE_ENTRIES(TypeBF16, 1, 256, 32, 4, 2))
+// (BN, NW, OCC) of the compiled tile shapes; overridable for tile sweeps.
+#ifndef RSFA_D256_TILES
+#define RSFA_D256_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 256, 32, 4, 2)
+#endif
+
+RSFA_DEFINE_KERNEL_LIST(kernels_d256, RSFA_D256_TILES(TypeF16, 0), RSFA_D256_TILES(TypeBF16, 1))

@@ -4,5 +4,9 @@
 
 using namespace rsfa;
 
-RSFA_DEFINE_KERNEL_LIST(kernels_d32,
-    RSFA_TILE_ENTRIES(TypeF16, 0, 32, 64, 4, 2), RSFA_TILE_ENTRIES(TypeBF16, 1, 32, 64, 4, 2))
+// (BN, NW, OCC) of the compiled tile shapes; overridable for tile sweeps.
+#ifndef RSFA_D32_TILES
+#define RSFA_D32_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 32, 64, 4, 2)
+#endif
+
+RSFA_DEFINE_KERNEL_LIST(kernels_d32, RSFA_D32_TILES(TypeF16, 0), RSFA_D32_TILES(TypeBF16, 1))

@@ -132,8 +132,9 @@ int resident_wgs(DeviceState& ds, const KernelEntry& e) {
 // Tile search.  The reference's get_tiling is a table of Ascend UB tilings
 // (flash_attention_forward.py:628-664) and its search tool times every
 // (BM, BN) pair (tiling/search_optimal_tiling.py:47-81).  Here the candidates
-// are the compiled instantiations for (dtype, head dim); each is checked
-// against gfx950's per-SIMD register file and per-CU LDS and scored with a
+// are the compiled instantiations for (dtype, head dim), each built for a
+// stated number of waves per SIMD; each is checked against gfx950's per-CU LDS
+// and scored with a
 // cost model: the persistent grid's makespan in key-tile steps, where a step of
 // a BM x BN tile costs its MFMA cycles plus a fixed per-tile synchronisation
 // overhead, and workgroups sharing a CU share its four SIMDs.
@@ -143,21 +144,13 @@ struct TileCost {
     double cycles;
 };
 
-int vgpr_estimate(const KernelEntry& e) {
-    const int dp = e.d < 32 ? 32 : e.d;
-    const int q = (e.d / 16) * 4;        // Q^T fragments
-    const int o = (dp / 32) * 16;        // O^T accumulators
-    const int s = (e.bn / 32) * 16;      // S^T accumulators
-    const int pk = (e.bn / 32) * 8;      // packed P
-    return q + o + s + pk + 40;          // addresses, softmax state, fragments in flight
-}
-
 TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int num_cus) {
     TileCost tc{false, 0.0};
     const int dp = e.d < 32 ? 32 : e.d;
+    // Each instantiation was compiled for `occ` waves per SIMD (the compiler
+    // fits its registers to that), so only the LDS budget is checked here.
     const int lds = 2 * 2 * e.bn * dp * 2;
-    const int budget = 512 / e.occ;
-    if (vgpr_estimate(e) > budget || lds > kLdsPerCu) return tc;
+    if (lds > kLdsPerCu) return tc;
     const int wg_by_waves = (4 * e.occ) / e.nw;
     const int wg_by_lds = kLdsPerCu / lds;
     const int wg_per_cu = std::max(1, std::min(wg_by_waves, wg_by_lds));
