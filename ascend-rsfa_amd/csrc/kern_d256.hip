@@ -6,7 +6,7 @@ using namespace rsfa;
 
 // (BN, NW, OCC) of the compiled tile shapes; overridable for tile sweeps.
 #ifndef RSFA_D256_TILES
-#define RSFA_D256_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 256, 32, 4, 2)
+#define RSFA_D256_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 256, 32, 8, 2), RSFA_TILE_ENTRIES(T, DTYPE, 256, 32, 4, 2)
 #endif
 
 RSFA_DEFINE_KERNEL_LIST(kernels_d256, RSFA_D256_TILES(TypeF16, 0), RSFA_D256_TILES(TypeBF16, 1))

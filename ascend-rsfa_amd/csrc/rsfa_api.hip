@@ -144,6 +144,19 @@ struct TileCost {
     double cycles;
 };
 
+// SIMD-cycle model of one wave's key-tile step, measured on MI355X: the two
+// contractions (32 x BN x D each at 1024 flop/cycle) plus the softmax VALU work
+// (~9.5 cycles per score of the lane's 32 x BN tile share) plus workgroup
+// synchronisation, which costs an 8-wave workgroup (one per CU, two waves of
+// it per SIMD) about a third of what two 4-wave workgroups per CU pay.
+double wave_tile_cycles(const KernelEntry& e) {
+    const int dp = e.d < 32 ? 32 : e.d;
+    const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0;
+    const double valu = 9.5 * e.bn / 2.0 + 300.0 * e.bn / 64.0;
+    const double sync = e.nw >= 8 ? 100.0 : 300.0;
+    return mfma + valu + sync;
+}
+
 TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int num_cus) {
     TileCost tc{false, 0.0};
     const int dp = e.d < 32 ? 32 : e.d;
@@ -156,22 +169,28 @@ TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int nu
     const int wg_per_cu = std::max(1, std::min(wg_by_waves, wg_by_lds));
     const int bm = 32 * e.nw;
     const int64_t nmb = (n + bm - 1) / bm;
+    // workgroups that actually share a CU: fewer tasks than CUs leave each alone
+    const int64_t ntask = z * h * nmb;
+    const int64_t conc = std::min<int64_t>(wg_per_cu, (ntask + num_cus - 1) / num_cus);
+    const int waves_per_simd = (int)std::max<int64_t>(1, conc * e.nw / 4);
     const int64_t tiles_full = (n + e.bn - 1) / e.bn;
-    // cycles one workgroup needs per key tile: two GEMMs of 32 x BN x D per wave
-    // at 1024 flop/cycle/SIMD, a wave per SIMD slot, plus sync overhead.
-    const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0 * e.nw / 4.0 * wg_per_cu;
-    const double step = mfma + 220.0;
-    double total = 0.0, longest = 0.0;
+    const double step = wave_tile_cycles(e);
+    // Makespan of the persistent grid: total wave work over the 4 SIMDs of
+    // every CU, but no shorter than the longest task, whose waves each share
+    // a SIMD with waves_per_simd - 1 others.
+    double work = 0.0, longest = 0.0;
     for (int64_t mb = 0; mb < nmb; ++mb) {
         const int64_t tiles = e.causal ? std::min<int64_t>(tiles_full, ((mb + 1) * bm + e.bn - 1) / e.bn) : tiles_full;
         const double c = tiles * step + 600.0;  // + task setup / epilogue
-        total += c;
-        longest = std::max(longest, c);
+        work += c * e.nw;
+        longest = std::max(longest, c * waves_per_simd);
     }
-    total *= (double)(z * h);
-    const double slots = (double)num_cus * wg_per_cu;
+    work *= (double)(z * h);
+    // SIMDs with work: each wave of a running task sits on its own SIMD
+    // until all 4 * num_cus are taken
+    const double busy_simds = std::min<double>(4.0 * num_cus, (double)ntask * e.nw);
     tc.feasible = true;
-    tc.cycles = std::max(total / slots, longest) / wg_per_cu;
+    tc.cycles = std::max(work / busy_simds, longest);
     return tc;
 }
 
