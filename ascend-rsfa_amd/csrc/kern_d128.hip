@@ -6,7 +6,9 @@ using namespace rsfa;
 
 // (BN, NW, OCC) of the compiled tile shapes; overridable for tile sweeps.
 #ifndef RSFA_D128_TILES
-#define RSFA_D128_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 8, 2), RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 4, 2)
+#define RSFA_D128_TILES(T, DTYPE)                                                                        \
+    RSFA_TILE_ENTRIES(T, DTYPE, 128, 128, 8, 2), RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 8, 2), \
+        RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 4, 2)
 #endif
 
 RSFA_DEFINE_KERNEL_LIST(kernels_d128, RSFA_D128_TILES(TypeF16, 0), RSFA_D128_TILES(TypeBF16, 1))

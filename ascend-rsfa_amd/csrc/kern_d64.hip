@@ -6,7 +6,7 @@ using namespace rsfa;
 
 // (BN, NW, OCC) of the compiled tile shapes; overridable for tile sweeps.
 #ifndef RSFA_D64_TILES
-#define RSFA_D64_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 64, 64, 4, 2)
+#define RSFA_D64_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 64, 128, 8, 2), RSFA_TILE_ENTRIES(T, DTYPE, 64, 64, 4, 2)
 #endif
 
 RSFA_DEFINE_KERNEL_LIST(kernels_d64, RSFA_D64_TILES(TypeF16, 0), RSFA_D64_TILES(TypeBF16, 1))
