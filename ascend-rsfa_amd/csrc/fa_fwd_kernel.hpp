@@ -237,6 +237,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 #ifndef RSFA_PV_PREFETCH
 #define RSFA_PV_PREFETCH 4
 #endif
+#ifndef RSFA_PINGPONG
+#define RSFA_PINGPONG 1
+#endif
 constexpr int QK_PREFETCH = RSFA_QK_PREFETCH;
 constexpr int PV_PREFETCH = RSFA_PV_PREFETCH;
 
@@ -268,9 +271,36 @@ __device__ __forceinline__ void lgkm_wait2(V& a, V& b) {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
 }
 
+// A workgroup barrier that the compiler's scheduler does not move work across
+// (the ping-pong phases must not leak into each other).  No memory fence: the
+// LDS reads before it have all been waited for, and the direct loads are
+// tracked with explicit vmcnt waits.
+__device__ __forceinline__ void phase_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// LDS reads still outstanding once the reads of op m of an operand stream have
+// completed, when ops [0, min(m + pf, nops)) have been issued and ops below npv
+// take two reads each, the others one.
+constexpr int x_reads_after(int npv, int nops, int pf, int m) {
+    int n = 0;
+    for (int q = m + 1; q < m + pf && q < nops; ++q) n += q < npv ? 2 : 1;
+    return n;
+}
+
 __device__ __forceinline__ void wait_loads_and_sync() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+}
+
+// Whether an instantiation runs the ping-pong schedule (8-wave workgroups,
+// three K/V buffers within the 160 KB of LDS of a CU; head dims up to 128,
+// since at 256 the O^T and Q^T registers leave too few for the schedule).
+constexpr bool uses_pingpong(int d, int bn, int nw, int mode) {
+    return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && d <= 128 &&
+           3 * (2 * bn * (d < 32 ? 32 : d) * 2) <= 160 * 1024 - 64;
 }
 
 template <class T, int D, int BN, int NW, bool CAUSAL, int MODE, int OCC>
@@ -296,8 +326,14 @@ fa_fwd_kernel(FwdParams p) {
     static_assert(D % 16 == 0, "D must be a multiple of 16");
     static_assert((BN * CPR) % 64 == 0, "tile must be whole 1-KB load slices");
     static_assert(MODE == MODE_FUSED || CAUSAL, "split modes are causal only");
+    // Ping-pong schedule for 8-wave workgroups (two waves per SIMD): the key
+    // tiles every row of the workgroup sees unmasked run with waves 4-7 one
+    // phase behind waves 0-3, so one wave of each SIMD runs its softmax (VALU)
+    // while the other runs its matrix products.  K/V are triple buffered.
+    constexpr bool PP = uses_pingpong(D, BN, NW, MODE);
+    constexpr int NBUF = PP ? 3 : 2;
 
-    __shared__ __attribute__((aligned(1024))) char smem_raw[2 * BUF];
+    __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
     __shared__ int s_ticket;
     RSFA_LDS char* const smem = (RSFA_LDS char*)smem_raw;
     const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
@@ -426,7 +462,10 @@ fa_fwd_kernel(FwdParams p) {
             }
         };
 
-        if (j0 < j1) load_tile(j0, 0);
+        // [j0, jpp): ping-pong tiles (whole tiles no row of the workgroup masks)
+        int jpp = j0;
+        if constexpr (PP) jpp = min(j1, (CAUSAL ? m0 : n) / BN);
+        if (jpp == j0 && j0 < j1) load_tile(j0, 0);
 
         // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
         // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
@@ -472,12 +511,12 @@ fa_fwd_kernel(FwdParams p) {
         const int vis_lo = CAUSAL ? min(wq_lo, n - 1) : n - 1;  // last key every lane of the wave sees
         const int vis_hi = CAUSAL ? min(wq_hi, n - 1) : n - 1;  // last key any lane of the wave sees
 
-        // one key tile: S^T, softmax update, O^T += V^T P^T
-        auto tile_step = [&](int buf, int kbase, int nkt_act, auto masked) {
+        // S^T = K Q^T for the key tile whose K sits at LDS byte offset kofs.
+        // Masked: keys past each row's last visible key become -inf, and 32-key
+        // sub-tiles at or past nkt_act (no row of the wave sees them) are skipped.
+        auto qk_part = [&](uint32_t kofs, int kbase, int nkt_act, f32x16 (&sacc)[NKT], auto masked) {
             constexpr bool MASK = decltype(masked)::value;
-            const RSFA_LDS char* kt_lds = smem + buf * BUF;
-            const RSFA_LDS char* vt_lds = kt_lds + TILE;
-            f32x16 sacc[NKT];
+            const RSFA_LDS char* kt_lds = smem + kofs;
             const f32x16 zero = {};  // the first k-step adds to an inline-constant 0
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) sacc[kt] = zero;
@@ -486,8 +525,8 @@ fa_fwd_kernel(FwdParams p) {
                 constexpr int NM = KST * NKT;
                 constexpr int PF = QK_PREFETCH < NM ? QK_PREFETCH : NM;
                 constexpr int NB = PF + 1;
-                const uint32_t kb0 = smem_addr + buf * BUF + koff[0];
-                const uint32_t kb1 = smem_addr + buf * BUF + koff[1];
+                const uint32_t kb0 = smem_addr + kofs + koff[0];
+                const uint32_t kb1 = smem_addr + kofs + koff[1];
                 i32x4 ring[NB];
                 auto issue = [&](auto ic) {
                     constexpr int i = decltype(ic)::value;
@@ -525,6 +564,12 @@ fa_fwd_kernel(FwdParams p) {
                         if (kk > rel || kt >= nkt_act) sacc[kt][r] = -INFINITY;
                     }
             }
+        };
+        // Online softmax of one S^T tile: fold its row max into m_use (rescaling
+        // O and l when it moves), P = exp2(S c - m) rounded to the input type
+        // into pk, and the row sum of the rounded P into l_sum.
+        auto softmax_part = [&](f32x16 (&sacc)[NKT], x8 (&pk)[NKT][2], auto masked) {
+            constexpr bool MASK = decltype(masked)::value;
             float mx = sacc[0][0];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
@@ -545,7 +590,6 @@ fa_fwd_kernel(FwdParams p) {
                 m_use = m_new;
             }
             const float msub = (MASK && m_use == -INFINITY) ? 0.0f : m_use;
-            x8 pk[NKT][2];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) {
 #pragma unroll
@@ -561,13 +605,18 @@ fa_fwd_kernel(FwdParams p) {
                     pk[kt][h2] = (x8){pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
                 }
             }
+        };
+        // O^T += V^T P^T for the value tile at LDS byte offset vofs.
+        auto pv_part = [&](uint32_t vofs, int nkt_act, const x8 (&pk)[NKT][2], auto masked) {
+            constexpr bool MASK = decltype(masked)::value;
+            const RSFA_LDS char* vt_lds = smem + vofs;
             if (!MASK) {
                 // MFMA i = (d, kt, h2), i = (d*NKT + kt)*2 + h2, two transposing reads each
                 constexpr int NM = DT * NKT * 2;
                 constexpr int PF = PV_PREFETCH < NM ? PV_PREFETCH : NM;
                 constexpr int NB = PF + 1;
-                const uint32_t vb0 = smem_addr + buf * BUF + TILE + voff[0];
-                const uint32_t vb1 = smem_addr + buf * BUF + TILE + voff[1];
+                const uint32_t vb0 = smem_addr + vofs + voff[0];
+                const uint32_t vb1 = smem_addr + vofs + voff[1];
                 // the two halves stay separate registers until their wait: a
                 // copy into one 4-register operand before it would read them early
                 i32x2 rlo[NB], rhi[NB];
@@ -607,21 +656,169 @@ fa_fwd_kernel(FwdParams p) {
             }
             }
         };
+        // one key tile in LDS buffer buf: S^T, softmax update, O^T += V^T P^T
+        auto tile_step = [&](int buf, int kbase, int nkt_act, auto masked) {
+            f32x16 sacc[NKT];
+            x8 pk[NKT][2];
+            qk_part((uint32_t)(buf * BUF), kbase, nkt_act, sacc, masked);
+            softmax_part(sacc, pk, masked);
+            pv_part((uint32_t)(buf * BUF + TILE), nkt_act, pk, masked);
+        };
 
-        // Key tiles [j0, ju) are visible to every row of this wave (mask-free
+        int j = j0;
+        if constexpr (PP) {
+            if (jpp > j0) {
+                // Phases are cut by barriers.  Every wave runs the same code:
+                //   X_t: PV(t-1) then QK(t), and the loads of K_{t+2}, V_{t+1}
+                //   Y_t: softmax(t)
+                // and waves 4-7 pass one extra barrier first, so while waves
+                // 0-3 run X_t the others run Y_{t-1}, and while 0-3 run Y_t the
+                // others run X_t.  Because of that one-phase lag, data waited
+                // for (vmcnt) at some point of the code is read only after two
+                // more barriers of the code, and a buffer is refilled only two
+                // barriers after its last read.  With three buffers: X_t waits
+                // for the loads of X_{t-1} and then refills the buffers of
+                // K_{t-1} and V_{t-2}, last read in X_{t-1}; X_{t+1} reads V_t
+                // and K_{t+1}.  The loads sit among the last MFMAs of the phase,
+                // where they do not hold up the softmax of the other waves.
+                const int grp = wave >= NW / 2 ? 1 : 0;
+                // the MFMA phase's wave is issued first when both waves of a SIMD are ready
+                auto prio_mfma = [&]() { __builtin_amdgcn_s_setprio(1); };
+                auto prio_valu = [&]() { __builtin_amdgcn_s_setprio(0); };
+                const std::false_type mask_free;
+                auto bofs = [&](int jj) { return (uint32_t)((jj % NBUF) * BUF); };
+                // slice sl of this wave's share of tile jj of K (or V)
+                auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
+                    const int w = sl * NW + wave;
+                    if (NINST % NW == 0 || w < NINST) {
+                        const int cg = ((w * 64) % (16 * CPR)) / 64;
+                        if (CPRV == CPR || 4 * cg + ld_chl < CPRV)
+                            dma16(th + (int64_t)(jj * BN) * sn, go[sl], dst0 + w * 1024);
+                    }
+                };
+                auto dma_k = [&](int jj, int sl) { pp_dma(kh, p.k_sn, kgo, jj, smem_addr + bofs(jj), sl); };
+                auto dma_v = [&](int jj, int sl) { pp_dma(vh, p.v_sn, vgo, jj, smem_addr + bofs(jj) + TILE, sl); };
+                auto load_k = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_k(jj, sl); };
+                auto load_v = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_v(jj, sl); };
+
+                // One X phase is a single stream of MFMAs, op m < NPV being
+                // PV MFMA m (two transposing reads) and op NPV + i QK MFMA i
+                // (one read); each op's reads are issued XPF ops ahead.
+                constexpr int NPV = DT * NKT * 2;
+                constexpr int NQK = KST * NKT;
+                constexpr int XPF = PV_PREFETCH;
+                constexpr int XNB = XPF + 1;
+                constexpr int NDMA = 2 * NSL;  // direct loads per wave per X phase
+                constexpr int DSTEP = 2;       // MFMAs between them
+                i32x2 rlo[XNB], rhi[XNB];
+                i32x4 kr[XNB];
+                uint32_t xa[4];  // V reads (two halves), K reads (even / odd k-steps)
+                auto x_issue = [&](auto mc) {
+                    constexpr int m = decltype(mc)::value;
+                    if constexpr (m < NPV) {
+                        constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
+                        constexpr int off = (2 * kt + h2) * BLK + d * 1024;
+                        rlo[m % XNB] = lds_read_tr16<off>(xa[0]);
+                        rhi[m % XNB] = lds_read_tr16<off>(xa[1]);
+                    } else {
+                        constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
+                        kr[i % XNB] = lds_read_b128<kt * 2 * BLK + ss * 512>(xa[2 + (ss & 1)]);
+                    }
+                };
+                // X phase of PV(tv) and, when M > NPV, QK(tv + 1); with tl >= 0 it
+                // first waits for the loads of the previous X phase, then loads
+                // K_{tl+1} (if tl + 1 < jpp) and V_tl (if tl < jpp).
+                auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT]) {
+                    constexpr int M = decltype(nm)::value;
+                    constexpr int D0 = M - NDMA * DSTEP;
+                    static_assert(D0 >= 0, "operand stream shorter than its loads");
+                    xa[0] = smem_addr + bofs(tv) + TILE + voff[0];
+                    xa[1] = smem_addr + bofs(tv) + TILE + voff[1];
+                    xa[2] = smem_addr + bofs(tv + 1) + koff[0];
+                    xa[3] = smem_addr + bofs(tv + 1) + koff[1];
+                    static_for<(XPF < M ? XPF : M)>(x_issue);
+                    const f32x16 zero = {};
+                    static_for<M>([&](auto mc) {
+                        constexpr int m = decltype(mc)::value;
+                        constexpr int N = x_reads_after(NPV, M, XPF, m);
+                        if constexpr (m < NPV) {
+                            constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
+                            lgkm_wait2<N>(rlo[m % XNB], rhi[m % XNB]);
+                            const i32x2 lo = rlo[m % XNB], hi = rhi[m % XNB];
+                            o[d] = T::mfma(__builtin_bit_cast(x8, (i32x4){lo[0], lo[1], hi[0], hi[1]}), pk[kt][h2], o[d]);
+                        } else {
+                            constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
+                            lgkm_wait<N>(kr[i % XNB]);
+                            sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss], ss == 0 ? zero : sacc[kt]);
+                        }
+                        if constexpr (m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
+                        if constexpr (m >= D0 && (m - D0) % DSTEP == 0) {
+                            constexpr int q = (m - D0) / DSTEP;
+                            if (tl >= 0) {
+                                if constexpr (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                                if constexpr (q < NSL) {
+                                    if (tl + 1 < jpp) dma_k(tl + 1, q);
+                                } else {
+                                    if (tl < jpp) dma_v(tl, q - NSL);
+                                }
+                            }
+                        }
+                    });
+                };
+
+                load_k(j0);
+                load_v(j0);
+                if (j0 + 1 < jpp) load_k(j0 + 1);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                if (grp) phase_barrier();
+                phase_barrier();  // X_j0: QK only, then the loads of K_{j0+2}, V_{j0+1}
+                prio_mfma();
+                f32x16 sacc[NKT];
+                qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free);
+                if (j0 + 2 < jpp) load_k(j0 + 2);
+                if (j0 + 1 < jpp) load_v(j0 + 1);
+                int t = j0;
+                for (; t + 1 < jpp; ++t) {
+                    phase_barrier();  // Y_t
+                    prio_valu();
+                    x8 pk[NKT][2];
+                    softmax_part(sacc, pk, mask_free);
+                    phase_barrier();  // X_{t+1}
+                    prio_mfma();
+                    x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc);
+                }
+                {
+                    phase_barrier();  // Y of the last tile
+                    prio_valu();
+                    x8 pk[NKT][2];
+                    softmax_part(sacc, pk, mask_free);
+                    phase_barrier();  // its PV
+                    prio_mfma();
+                    x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc);
+                    prio_valu();
+                }
+                if (!grp) phase_barrier();
+                // realigned; the remaining tiles use buffers 0 and 1
+                __syncthreads();
+                j = jpp;
+                if (j < j1) load_tile(j, 0);
+            }
+        }
+
+        // Key tiles [jr, ju) are visible to every row of this wave (mask-free
         // body); [ju, j1) straddle the causal diagonal or the sequence end.
         // Both loops run the same barrier sequence in every wave.
+        const int jr = j;
         int ju = min(j1, (vis_lo + 1) / BN);
-        ju = max(ju, j0);
-        int j = j0;
+        ju = max(ju, jr);
         for (; j < ju; ++j) {
-            const int buf = (j - j0) & 1;
+            const int buf = (j - jr) & 1;
             wait_loads_and_sync();
             if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
             tile_step(buf, j * BN, NKT, std::integral_constant<bool, false>());
         }
         for (; j < j1; ++j) {
-            const int buf = (j - j0) & 1;
+            const int buf = (j - jr) & 1;
             wait_loads_and_sync();
             if (j + 1 < j1) load_tile(j + 1, buf ^ 1);
             const int kbase = j * BN;

@@ -15,6 +15,7 @@ struct KernelEntry {
     int causal;  // 0 / 1
     int mode;    // MODE_FUSED / MODE_PREFIX / MODE_DIAG
     int occ;     // waves per SIMD the kernel was register-budgeted for
+    int pp;      // 1: ping-pong schedule (three K/V buffers)
     const void* fn;
 };
 
@@ -32,11 +33,13 @@ KernelList kernels_d256();
 }  // namespace rsfa
 
 // One tile configuration: non-causal fused, causal fused, causal prefix, causal diagonal.
-#define RSFA_TILE_ENTRIES(T, DTYPE, D, BN, NW, OCC)                                                          \
-    {DTYPE, D, BN, NW, 0, MODE_FUSED, OCC, (const void*)&fa_fwd_kernel<T, D, BN, NW, false, MODE_FUSED, OCC>}, \
-    {DTYPE, D, BN, NW, 1, MODE_FUSED, OCC, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_FUSED, OCC>},  \
-    {DTYPE, D, BN, NW, 1, MODE_PREFIX, OCC, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_PREFIX, OCC>}, \
-    {DTYPE, D, BN, NW, 1, MODE_DIAG, OCC, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_DIAG, OCC>}
+#define RSFA_TILE_ENTRIES(T, DTYPE, D, BN, NW, OCC)                                                  \
+    {DTYPE, D, BN, NW, 0, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, MODE_FUSED),                          \
+     (const void*)&fa_fwd_kernel<T, D, BN, NW, false, MODE_FUSED, OCC>},                                  \
+    {DTYPE, D, BN, NW, 1, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, MODE_FUSED),                          \
+     (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_FUSED, OCC>},                                   \
+    {DTYPE, D, BN, NW, 1, MODE_PREFIX, OCC, 0, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_PREFIX, OCC>}, \
+    {DTYPE, D, BN, NW, 1, MODE_DIAG, OCC, 0, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_DIAG, OCC>}
 
 #define RSFA_DEFINE_KERNEL_LIST(NAME, ...)                                   \
     namespace rsfa {                                                         \

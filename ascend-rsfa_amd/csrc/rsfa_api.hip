@@ -148,11 +148,13 @@ struct TileCost {
 // contractions (32 x BN x D each at 1024 flop/cycle) plus the softmax VALU work
 // (~9.5 cycles per score of the lane's 32 x BN tile share) plus workgroup
 // synchronisation, which costs an 8-wave workgroup (one per CU, two waves of
-// it per SIMD) about a third of what two 4-wave workgroups per CU pay.
+// it per SIMD) about a third of what two 4-wave workgroups per CU pay.  The
+// ping-pong schedule hides about a quarter of the softmax work behind the
+// other wave's MFMAs.
 double wave_tile_cycles(const KernelEntry& e) {
     const int dp = e.d < 32 ? 32 : e.d;
     const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0;
-    const double valu = 9.5 * e.bn / 2.0 + 300.0 * e.bn / 64.0;
+    const double valu = (9.5 * e.bn / 2.0 + 300.0 * e.bn / 64.0) * (e.pp ? 0.75 : 1.0);
     const double sync = e.nw >= 8 ? 100.0 : 300.0;
     return mfma + valu + sync;
 }
@@ -162,7 +164,7 @@ TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int nu
     const int dp = e.d < 32 ? 32 : e.d;
     // Each instantiation was compiled for `occ` waves per SIMD (the compiler
     // fits its registers to that), so only the LDS budget is checked here.
-    const int lds = 2 * 2 * e.bn * dp * 2;
+    const int lds = (e.pp ? 3 : 2) * 2 * e.bn * dp * 2;
     if (lds > kLdsPerCu) return tc;
     const int wg_by_waves = (4 * e.occ) / e.nw;
     const int wg_by_lds = kLdsPerCu / lds;

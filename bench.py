@@ -138,8 +138,11 @@ def cpu_baseline(torch, cfg, budget_s=10.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # The GPU's clocks settle only after ~100 ms of sustained MFMA load (the
+    # first launches run at boost clocks, then dip below the steady state):
+    # the default warmup lets the timed steps see the steady state.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="time only this config name")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0)
