@@ -23,6 +23,10 @@ OFFLOAD_ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{fma,mul,add}_f32 in device code.  The host pass
 # warns that it does not know the feature; that warning is expected.
+# amdgpu-atomic-optimizer-strategy=None: the task queue's ticket atomic stays a
+# plain returning atomic whose result is waited for where it is used (the
+# optimizer's wave-aggregated form consumes it at once, exposing its latency at
+# the start of every task).
 HIPCC_FLAGS = [
     "--offload-arch=" + OFFLOAD_ARCH,
     "-O3",
@@ -30,6 +34,7 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-command-line-argument",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + os.path.join(REPO_ROOT, "include"),
 ]

@@ -462,18 +462,46 @@ fa_fwd_kernel(FwdParams p) {
             }
         };
 
-        // [j0, jpp): ping-pong tiles (whole tiles no row of the workgroup masks)
+        // Ping-pong buffers: tile jj of K and V in buffer jj % NBUF.
+        auto bofs = [&](int jj) { return (uint32_t)((jj % NBUF) * BUF); };
+        // slice sl of this wave's share of tile jj of K (or V)
+        auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
+            const int w = sl * NW + wave;
+            if (NINST % NW == 0 || w < NINST) {
+                const int cg = ((w * 64) % (16 * CPR)) / 64;
+                if (CPRV == CPR || 4 * cg + ld_chl < CPRV)
+                    dma16(th + (int64_t)(jj * BN) * sn, go[sl], dst0 + w * 1024);
+            }
+        };
+        auto dma_k = [&](int jj, int sl) { pp_dma(kh, p.k_sn, kgo, jj, smem_addr + bofs(jj), sl); };
+        auto dma_v = [&](int jj, int sl) { pp_dma(vh, p.v_sn, vgo, jj, smem_addr + bofs(jj) + TILE, sl); };
+        auto load_k = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_k(jj, sl); };
+        auto load_v = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_v(jj, sl); };
+
+        // [j0, jpp): ping-pong tiles (whole tiles no row of the workgroup masks).
+        // The first loads go out before the Q loads, so their latencies overlap.
         int jpp = j0;
         if constexpr (PP) jpp = min(j1, (CAUSAL ? m0 : n) / BN);
-        if (jpp == j0 && j0 < j1) load_tile(j0, 0);
+        if (jpp > j0) {
+            load_k(j0);
+            load_v(j0);
+            if (j0 + 1 < jpp) load_k(j0 + 1);
+        } else if (j0 < j1) {
+            load_tile(j0, 0);
+        }
 
         // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
         // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
         x8 qf[KST];
 #pragma unroll
         for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(qb + (int64_t)qrow_c * p.q_sm + (2 * s + hh) * 8);
+        if (qsign) {
+            // a real branch (the asm keeps it from being flattened into an xor
+            // with 0), so positive scales do not wait for Q here
+            asm volatile("");
 #pragma unroll
-        for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+            for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+        }
 
         f32x16 o[DT];
 #pragma unroll
@@ -565,10 +593,9 @@ fa_fwd_kernel(FwdParams p) {
                     }
             }
         };
-        // Online softmax of one S^T tile: fold its row max into m_use (rescaling
-        // O and l when it moves), P = exp2(S c - m) rounded to the input type
-        // into pk, and the row sum of the rounded P into l_sum.
-        auto softmax_part = [&](f32x16 (&sacc)[NKT], x8 (&pk)[NKT][2], auto masked) {
+        // Row max of the tile folded into m_use (rescaling O and l when it
+        // moves); returns the value to subtract before exp2.
+        auto softmax_max = [&](f32x16 (&sacc)[NKT], auto masked) {
             constexpr bool MASK = decltype(masked)::value;
             float mx = sacc[0][0];
 #pragma unroll
@@ -589,22 +616,26 @@ fa_fwd_kernel(FwdParams p) {
                     for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
                 m_use = m_new;
             }
-            const float msub = (MASK && m_use == -INFINITY) ? 0.0f : m_use;
-#pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) {
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2) {
-                    x2 pr[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i], c, -msub));
-                        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i + 1], c, -msub));
-                        pr[i] = T::cvt2(p0, p1);
-                        l_sum = T::dot2(pr[i], T::ones2(), l_sum);
-                    }
-                    pk[kt][h2] = (x8){pr[0][0], pr[0][1], pr[1][0], pr[1][1], pr[2][0], pr[2][1], pr[3][0], pr[3][1]};
-                }
-            }
+            return (MASK && m_use == -INFINITY) ? 0.0f : m_use;
+        };
+        // P for one pair of scores, unit u = (kt, h2, i) = ((kt*2 + h2)*4 + i):
+        // pk[kt][h2] elements 2i, 2i+1, and their rounded sum into l_sum.
+        auto softmax_unit = [&](auto uc, const f32x16 (&sacc)[NKT], x8 (&pk)[NKT][2], float msub) {
+            constexpr int u = decltype(uc)::value;
+            constexpr int kt = u / 8, h2 = (u / 4) % 2, i = u % 4;
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i], c, -msub));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i + 1], c, -msub));
+            const x2 pr = T::cvt2(p0, p1);
+            l_sum = T::dot2(pr, T::ones2(), l_sum);
+            pk[kt][h2][2 * i] = pr[0];
+            pk[kt][h2][2 * i + 1] = pr[1];
+        };
+        // Online softmax of one S^T tile: row max (softmax_max), then
+        // P = exp2(S c - m) rounded to the input type into pk and the row sum
+        // of the rounded P into l_sum.
+        auto softmax_part = [&](f32x16 (&sacc)[NKT], x8 (&pk)[NKT][2], auto masked) {
+            const float msub = softmax_max(sacc, masked);
+            static_for<NKT * 8>([&](auto uc) { softmax_unit(uc, sacc, pk, msub); });
         };
         // O^T += V^T P^T for the value tile at LDS byte offset vofs.
         auto pv_part = [&](uint32_t vofs, int nkt_act, const x8 (&pk)[NKT][2], auto masked) {
@@ -686,20 +717,6 @@ fa_fwd_kernel(FwdParams p) {
                 auto prio_mfma = [&]() { __builtin_amdgcn_s_setprio(1); };
                 auto prio_valu = [&]() { __builtin_amdgcn_s_setprio(0); };
                 const std::false_type mask_free;
-                auto bofs = [&](int jj) { return (uint32_t)((jj % NBUF) * BUF); };
-                // slice sl of this wave's share of tile jj of K (or V)
-                auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
-                    const int w = sl * NW + wave;
-                    if (NINST % NW == 0 || w < NINST) {
-                        const int cg = ((w * 64) % (16 * CPR)) / 64;
-                        if (CPRV == CPR || 4 * cg + ld_chl < CPRV)
-                            dma16(th + (int64_t)(jj * BN) * sn, go[sl], dst0 + w * 1024);
-                    }
-                };
-                auto dma_k = [&](int jj, int sl) { pp_dma(kh, p.k_sn, kgo, jj, smem_addr + bofs(jj), sl); };
-                auto dma_v = [&](int jj, int sl) { pp_dma(vh, p.v_sn, vgo, jj, smem_addr + bofs(jj) + TILE, sl); };
-                auto load_k = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_k(jj, sl); };
-                auto load_v = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_v(jj, sl); };
 
                 // One X phase is a single stream of MFMAs, op m < NPV being
                 // PV MFMA m (two transposing reads) and op NPV + i QK MFMA i
@@ -766,10 +783,7 @@ fa_fwd_kernel(FwdParams p) {
                     });
                 };
 
-                load_k(j0);
-                load_v(j0);
-                if (j0 + 1 < jpp) load_k(j0 + 1);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_j0, V_j0, K_j0+1
                 if (grp) phase_barrier();
                 phase_barrier();  // X_j0: QK only, then the loads of K_{j0+2}, V_{j0+1}
                 prio_mfma();
