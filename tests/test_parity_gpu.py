@@ -187,6 +187,25 @@ def test_every_output_row_written():
         assert bool(torch.isfinite(out).all())
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Z,H,N", [(2, 64, 1280), (1, 2, 1280), (4, 32, 2048)])
+def test_noncausal_many_and_few_tasks(D, dtype, Z, H, N):
+    """Non-causal launches of whole 256-row query blocks on the ping-pong
+    tiles: several tasks per workgroup (2x64x1280: 640 tasks), one (1x2x1280),
+    the C2-sized case; outputs and LSE of sampled heads against the oracle."""
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + D + H, dtype=dtype)
+    qd, kd, vd = _to_gpu(q, k, v)
+    out, lse = F.forward(qd, kd, vd, False, 1 / math.sqrt(D), return_lse=True)
+    out, lse = out.float().cpu(), lse.cpu()
+    assert bool(torch.isfinite(out).all())
+    heads = _sample_heads(Z, H, 6, seed=N + D)
+    ref, ref_lse = A.reference_attention(q, k, v, False, 1 / math.sqrt(D), return_lse=True, heads=heads)
+    for i, (b, h) in enumerate(heads):
+        _assert_close(out[b, h], ref[i], f"D={D} {dtype} Z={Z} H={H} N={N} head ({b},{h})")
+        assert (lse[b, h] - ref_lse[i]).abs().max().item() < 1e-3
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_dynamic_and_static_schedules_bitwise_equal(causal):
     q, k, v = A.make_inputs(4, 8, 1024, 128, seed=15)
