@@ -696,6 +696,13 @@ fa_fwd_kernel(FwdParams p) {
             pv_part((uint32_t)(buf * BUF + TILE), nkt_act, pk, masked);
         };
 
+        // Q has arrived by now as far as the compiler knows: the tile loops wait
+        // for the first tile's loads (issued before Q's) anyway, and without
+        // this it would wait for Q, i.e. for the newest direct loads, at
+        // every use of qf inside the loops.
+#pragma unroll
+        for (int s = 0; s < KST; ++s) asm volatile("" : "+v"(qf[s]));
+
         int j = j0;
         if constexpr (PP) {
             if (jpp > j0) {
