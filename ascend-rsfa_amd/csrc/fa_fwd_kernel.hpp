@@ -732,6 +732,15 @@ fa_fwd_kernel(FwdParams p) {
                 constexpr int NQK = KST * NKT;
                 constexpr int XPF = PV_PREFETCH;
                 constexpr int XNB = XPF + 1;
+                // The row sums of P (one dependent chain of VALU adds) are left
+                // to the compiler, which sinks them to the end of the next X
+                // phase, unless the softmax phase is the shorter one: the MFMA
+                // work of a phase grows with D, the softmax work does not.  At
+                // D = 128 the softmax waves wait ~500 cycles at each barrier for
+                // the MFMA waves, so the sums are pinned there (an empty asm that
+                // uses l_sum before the barrier); at D = 64 the softmax phase is
+                // the longer one (measured: +2 % at D = 128, -5 % at D = 64).
+                constexpr bool LSUM_IN_Y = D >= 128;
                 constexpr int NDMA = 2 * NSL;  // direct loads per wave per X phase
                 constexpr int DSTEP = 2;       // MFMAs between them
                 i32x2 rlo[XNB], rhi[XNB];
@@ -755,7 +764,7 @@ fa_fwd_kernel(FwdParams p) {
                 auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT]) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
-                    static_assert(D0 >= 0, "operand stream shorter than its loads");
+                    static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
                     xa[0] = smem_addr + bofs(tv) + TILE + voff[0];
                     xa[1] = smem_addr + bofs(tv) + TILE + voff[1];
                     xa[2] = smem_addr + bofs(tv + 1) + koff[0];
@@ -776,8 +785,11 @@ fa_fwd_kernel(FwdParams p) {
                             sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss], ss == 0 ? zero : sacc[kt]);
                         }
                         if constexpr (m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
-                        if constexpr (m >= D0 && (m - D0) % DSTEP == 0) {
+                        // load q of NDMA at op D0 + q * DSTEP (q < NDMA: the wave's K
+                        // slices, then its V slices)
+                        if constexpr (m >= D0 && m < D0 + NDMA * DSTEP && (m - D0) % DSTEP == 0) {
                             constexpr int q = (m - D0) / DSTEP;
+                            static_assert(q < NDMA, "load slot past the wave's slices");
                             if (tl >= 0) {
                                 if constexpr (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                                 if constexpr (q < NSL) {
@@ -804,6 +816,7 @@ fa_fwd_kernel(FwdParams p) {
                     prio_valu();
                     x8 pk[NKT][2];
                     softmax_part(sacc, pk, mask_free);
+                    if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc);
@@ -813,6 +826,7 @@ fa_fwd_kernel(FwdParams p) {
                     prio_valu();
                     x8 pk[NKT][2];
                     softmax_part(sacc, pk, mask_free);
+                    if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // its PV
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc);
