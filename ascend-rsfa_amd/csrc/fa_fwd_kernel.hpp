@@ -872,7 +872,44 @@ fa_fwd_kernel(FwdParams p) {
             }
         }
         const float inv = (MODE == MODE_PREFIX) ? (lt > 0.0f ? 1.0f / lt : 0.0f) : 1.0f / lt;
-        if (qrow < n) {
+        // O leaves through LDS when the workgroup's rows fit there: in the
+        // accumulator layout a lane holds 8 bytes of a row per (d, a), so a
+        // direct store instruction writes 32 rows x 16 bytes, and a CU needs
+        // ~64 cycles per such instruction (measured: the second group of
+        // waves waited ~4k cycles per task behind the first group's stores);
+        // staged row-major, each store instruction writes whole 16-byte
+        // chunks of 64 / (D / 8) consecutive rows (+2.5 to +3.6 % on C2, B=128,
+        // C3 and D=64).  D = 256 tiles do not fit and store directly.
+        constexpr int OROW = 2 * D + 16;  // bytes per staged row (16-byte pad)
+        constexpr bool OSTAGE = NW * 32 * OROW <= NBUF * BUF;
+        if constexpr (OSTAGE) {
+            __syncthreads();  // every wave is done with the K/V tiles
+            RSFA_LDS char* const ow = smem + wave * (32 * OROW);
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const int col = 32 * d + 8 * a + 4 * hh;
+                    if (col < D) {
+                        x4 v4;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v4[e] = (elem)(o[d][4 * a + e] * inv);
+                        *(RSFA_LDS x4*)(ow + l32 * OROW + col * 2) = v4;
+                    }
+                }
+            constexpr int CH = D / 8;     // 16-byte chunks per row
+            constexpr int RPI = 64 / CH;  // rows per store instruction
+            const int rr = lane / CH, cc = (lane % CH) * 8;
+            const int row0 = m0 + wave * 32;
+#pragma unroll
+            for (int it = 0; it < 32 / RPI; ++it) {
+                const int r = it * RPI + rr;
+                const x8 v = *(const RSFA_LDS x8*)(ow + r * OROW + cc * 2);
+                if (row0 + r < n) *(x8*)(ob + (int64_t)(row0 + r) * p.o_sm + cc) = v;
+            }
+            if (MODE != MODE_PREFIX && p.lse && hh == 0 && qrow < n)
+                p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;
+        } else if (qrow < n) {
 #pragma unroll
             for (int d = 0; d < DT; ++d)
 #pragma unroll
