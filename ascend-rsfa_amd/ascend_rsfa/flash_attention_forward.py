@@ -72,10 +72,23 @@ def get_tiling(Z, H, N_CTX, HEAD_DIM, causal):
     """Return (BLOCK_M, BLOCK_N) for the shape (reference 624-665).
 
     The reference looks the shape up in a table of Ascend tilings and raises
-    KeyError for any shape not listed; this searches the compiled gfx950 tile
-    shapes with a register/LDS feasibility check and a makespan model of the
+    KeyError for any shape not listed.  Here a measured, correctness-gated
+    tiling cache answers first when one is active (``tiling.use_cache`` or
+    ``RSFA_TILING_CACHE``; entries that are not a compiled tile shape are
+    ignored); otherwise the library searches the compiled gfx950 tile shapes
+    with a register/LDS feasibility check and a makespan model of the
     persistent grid, so it answers for every valid shape.
     """
+    from . import tiling
+    cache = tiling.active_cache()
+    if cache is not None:
+        hit = cache.lookup(Z, H, N_CTX, HEAD_DIM, causal)
+        if hit is not None:
+            try:
+                if resolve_tiling(HEAD_DIM, causal, hit[0], hit[1]) == tuple(hit):
+                    return tuple(hit)
+            except ValueError:
+                pass
     bm = ctypes.c_int32()
     bn = ctypes.c_int32()
     st = _native.lib().rsfa_get_tiling(int(Z), int(H), int(N_CTX), int(HEAD_DIM), 1 if causal else 0,
