@@ -9,7 +9,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "librsfa.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # rsfa_status
 OK = 0
@@ -27,6 +27,7 @@ E_WORKSPACE = -10
 # rsfa_dtype
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
+DTYPE_F16_V8E5M2 = 2  # q, k, o float16; v float8_e5m2
 
 # flags
 FLAG_STATIC_SCHEDULE = 0x1
@@ -70,6 +71,7 @@ class FwdArgs(ctypes.Structure):
 SIGNATURES = {
     "rsfa_attention_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "rsfa_split_workspace_bytes": (ctypes.c_uint64, [_I64, _I64, _I64, _I64, _I32]),
+    "rsfa_v8_workspace_bytes": (ctypes.c_uint64, [_I64, _I64, _I64, _I64]),
     "rsfa_get_tiling": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32]),
     "rsfa_resolve_tiling": (ctypes.c_int, [_I64, _I32, _I32, _I32, _I32, _PI32, _PI32]),
     "rsfa_get_num_compute_cores": (ctypes.c_int, [ctypes.c_int]),

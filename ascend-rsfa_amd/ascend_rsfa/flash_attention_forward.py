@@ -22,6 +22,11 @@ All arithmetic runs in the HIP library ``lib/librsfa.so`` (C ABI in
 device.  There is no fallback path: without the built library, or for tensors
 that are not on a GPU, the calls raise.
 
+A ``float8_e5m2`` V with float16 Q and K runs the reference's fp8_v branch
+(_attn_fwd_inner 208-211, 217): P is rounded to e5m2 for P.V while the row
+sums add the unrounded P; O is float16.  The library widens V to fp16 in a
+workspace first (exact: an e5m2 byte is the high byte of that fp16).
+
 Behaviour beyond the reference (documented, deliberate):
 
 * ``BM``/``BN`` keep the reference's meaning (query rows per program, keys per
@@ -44,6 +49,7 @@ __all__ = ["attention", "get_tiling", "get_num_compute_cores", "resolve_tiling",
            "split_workspace_bytes"]
 
 _DTYPES = {torch.float16: _native.DTYPE_F16, torch.bfloat16: _native.DTYPE_BF16}
+_FP8_E5M2 = getattr(torch, "float8_e5m2", None)
 
 
 def _raise_for(status):
@@ -112,8 +118,10 @@ def split_workspace_bytes(Z, H, N_CTX, HEAD_DIM, BM):
 
 
 def _meets_contract(t):
+    # 16-byte rows: outer strides a multiple of 8 two-byte or 16 one-byte elements
+    mult = 16 // t.element_size()
     st = t.stride()
-    return st[3] == 1 and all(s % 8 == 0 for s in st[:3]) and t.data_ptr() % 16 == 0
+    return st[3] == 1 and all(s % mult == 0 for s in st[:3]) and t.data_ptr() % 16 == 0
 
 
 def _as_kernel_layout(t):
@@ -138,8 +146,10 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError(f"q, k, v must share one 4-D shape [Z, H, N_CTX, D]; got "
                          f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
-    if not (q.dtype == k.dtype == v.dtype):
-        raise TypeError("q, k and v must have the same dtype")
+    # a float8 e5m2 V with float16 Q, K takes the reference's fp8_v branch (208-211)
+    v8 = v.dtype == _FP8_E5M2 and q.dtype == torch.float16 and k.dtype == torch.float16
+    if not v8 and not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k and v must have the same dtype (or float16 q, k with a float8_e5m2 v)")
     if q.dtype not in _DTYPES:
         raise TypeError(f"unsupported dtype {q.dtype}; float16 and bfloat16 are supported")
     if not (q.is_cuda and k.is_cuda and v.is_cuda) or not (q.device == k.device == v.device):
@@ -157,7 +167,7 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
 
     args = _native.FwdArgs()
     args.struct_size = ctypes.sizeof(_native.FwdArgs)
-    args.dtype = _DTYPES[q.dtype]
+    args.dtype = _native.DTYPE_F16_V8E5M2 if v8 else _DTYPES[q.dtype]
     args.q, args.k, args.v, args.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
     args.lse = lse.data_ptr() if lse is not None else None
     args.z, args.h, args.n_ctx, args.head_dim = Z, H, N, D
@@ -171,13 +181,16 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
         _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0)
     ws = None
     with torch.cuda.device(q.device):
+        # workspace: the fp16 copy of a float8 V, then the split state
+        nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0
         if split and causal:
             bm = BM
             if not (BM or BN):
                 bm, _ = get_tiling(Z, H, N, D, causal)
             else:
                 bm, _ = resolve_tiling(D, causal, BM, BN, q.dtype)
-            nbytes = split_workspace_bytes(Z, H, N, D, bm)
+            nbytes += split_workspace_bytes(Z, H, N, D, bm)
+        if nbytes:
             ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
             args.workspace = ws.data_ptr()
             args.workspace_bytes = nbytes

@@ -63,6 +63,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 constexpr float RESCALE_SLACK = 8.0f;
 
 struct TypeF16 {
+    static constexpr bool p8 = false;  // P rounded to the input dtype
     typedef _Float16 elem;
     typedef _Float16 x8 __attribute__((ext_vector_type(8)));
     typedef _Float16 x4 __attribute__((ext_vector_type(4)));
@@ -84,6 +85,7 @@ struct TypeF16 {
 };
 
 struct TypeBF16 {
+    static constexpr bool p8 = false;
     typedef __bf16 elem;
     typedef __bf16 x8 __attribute__((ext_vector_type(8)));
     typedef __bf16 x4 __attribute__((ext_vector_type(4)));
@@ -102,6 +104,22 @@ struct TypeBF16 {
         return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
     }
     static __device__ __forceinline__ x2 ones2() { return (x2){(elem)1.0f, (elem)1.0f}; }
+};
+
+// fp16 Q, K, O with a float8 e5m2 V (reference flash_attention_forward.py:
+// 208-211, 253-256, 453-456: when V is float8e5, P is cast to float8e5 for
+// P.V, while the row sum l adds the unrounded P, 217 and 466).  The launcher
+// widens V to fp16 (exact: an e5m2 byte is the high byte of the fp16 with the
+// same value) and this type rounds P to e5m2 and widens it back the same way,
+// so the fp16 MFMA forms exactly the products of the e5m2 operands.
+struct TypeF16P8 : TypeF16 {
+    static constexpr bool p8 = true;
+    static __device__ __forceinline__ x2 cvt2(float a, float b) {
+        // two e5m2 bytes (round to nearest even) in bits 0-15 ...
+        const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+        // ... become the high bytes of two fp16
+        return __builtin_bit_cast(x2, ((w << 8) & 0xFF00u) | ((w << 16) & 0xFF000000u));
+    }
 };
 
 // Kernel modes.  MODE_FUSED runs every key tile of a task in one launch (the
@@ -626,7 +644,10 @@ fa_fwd_kernel(FwdParams p) {
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i], c, -msub));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i + 1], c, -msub));
             const x2 pr = T::cvt2(p0, p1);
-            l_sum = T::dot2(pr, T::ones2(), l_sum);
+            if constexpr (T::p8)
+                l_sum += p0 + p1;  // the reference sums the unrounded P for an e5m2 V
+            else
+                l_sum = T::dot2(pr, T::ones2(), l_sum);
             pk[kt][h2][2 * i] = pr[0];
             pk[kt][h2][2 * i + 1] = pr[1];
         };

@@ -1,4 +1,4 @@
-// Instantiations of the forward kernel for head dim 128 (fp16 and bf16).
+// Instantiations of the forward kernel for head dim 128 (fp16, bf16, and fp16 with a float8 e5m2 V).
 #include "fa_fwd_kernel.hpp"
 #include "kernel_table.hpp"
 
@@ -11,4 +11,5 @@ using namespace rsfa;
         RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 4, 2)
 #endif
 
-RSFA_DEFINE_KERNEL_LIST(kernels_d128, RSFA_D128_TILES(TypeF16, 0), RSFA_D128_TILES(TypeBF16, 1))
+RSFA_DEFINE_KERNEL_LIST(kernels_d128, RSFA_D128_TILES(TypeF16, 0), RSFA_D128_TILES(TypeBF16, 1),
+                        RSFA_D128_TILES(TypeF16P8, 2))

@@ -1,4 +1,4 @@
-// Instantiations of the forward kernel for head dim 32 (fp16 and bf16).
+// Instantiations of the forward kernel for head dim 32 (fp16, bf16, and fp16 with a float8 e5m2 V).
 #include "fa_fwd_kernel.hpp"
 #include "kernel_table.hpp"
 
@@ -9,4 +9,5 @@ using namespace rsfa;
 #define RSFA_D32_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 32, 64, 4, 2)
 #endif
 
-RSFA_DEFINE_KERNEL_LIST(kernels_d32, RSFA_D32_TILES(TypeF16, 0), RSFA_D32_TILES(TypeBF16, 1))
+RSFA_DEFINE_KERNEL_LIST(kernels_d32, RSFA_D32_TILES(TypeF16, 0), RSFA_D32_TILES(TypeBF16, 1),
+                        RSFA_D32_TILES(TypeF16P8, 2))

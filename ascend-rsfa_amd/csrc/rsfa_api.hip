@@ -235,14 +235,50 @@ int resolve(int64_t d, int causal, int dtype, int req_bm, int req_bn, const Kern
     return RSFA_OK;
 }
 
-int check_tensor(const void* ptr, const int64_t st[4]) {
+bool valid_dtype(int dt) {
+    return dt == RSFA_DTYPE_F16 || dt == RSFA_DTYPE_BF16 || dt == RSFA_DTYPE_F16_V8E5M2;
+}
+
+// `mult`: required multiple (elements) of the outer strides: 8 for 2-byte
+// elements, 16 for a float8 V, i.e. 16-byte rows either way.
+int check_tensor(const void* ptr, const int64_t st[4], int mult = 8) {
     if (((uintptr_t)ptr & 15) != 0) return RSFA_E_ALIGN;
     if (st[3] != 1) return RSFA_E_ALIGN;
     for (int i = 0; i < 3; ++i)
-        if (st[i] < 0 || (st[i] & 7) != 0) return RSFA_E_ALIGN;
+        if (st[i] < 0 || (st[i] % mult) != 0) return RSFA_E_ALIGN;
     // per-lane 32-bit byte offsets of the LDS loader cover 16 rows
     if (st[2] >= (int64_t(1) << 25)) return RSFA_E_ALIGN;
     return RSFA_OK;
+}
+
+// Widens a float8 e5m2 V [Z, H, N, D] (strided, unit head-dim stride) into a
+// contiguous fp16 copy.  An e5m2 byte is the high byte of the fp16 of the same
+// value (same sign, exponent bias 15, two leading mantissa bits), so the copy
+// is exact.  One thread per 16 input bytes, grid-stride.
+__global__ void __launch_bounds__(256) widen_v8(const uint8_t* __restrict__ v, int64_t sz, int64_t sh,
+                                                int64_t sn, int32_t h, int32_t n, int32_t d,
+                                                int64_t chunks, uint32_t* __restrict__ out) {
+    const int cpr = d / 16;  // 16-byte chunks per row
+    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < chunks;
+         c += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = c / cpr;  // (z * h + hh) * n + m
+        const int ch = (int)(c - row * cpr);
+        const int64_t bh = row / n;
+        const int m = (int)(row - bh * n);
+        const int64_t z = bh / h;
+        const int hh = (int)(bh - z * h);
+        const uint4 w = *(const uint4*)(v + z * sz + hh * sh + (int64_t)m * sn + ch * 16);
+        const uint32_t in[4] = {w.x, w.y, w.z, w.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i] = ((in[i] << 8) & 0xFF00u) | ((in[i] << 16) & 0xFF000000u);
+            o[2 * i + 1] = ((in[i] >> 8) & 0xFF00u) | (in[i] & 0xFF000000u);
+        }
+        uint4* dst = (uint4*)(out + c * 8);
+        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
 }
 
 }  // namespace
@@ -260,7 +296,7 @@ const char* rsfa_strerror(int status) {
         case RSFA_E_NULL: return "a required pointer is NULL";
         case RSFA_E_SHAPE: return "invalid shape: Z, H and N_CTX must be >= 1 and fit the 32-bit task index";
         case RSFA_E_HEADDIM: return "head_dim must be one of 16, 32, 64, 128, 256";
-        case RSFA_E_DTYPE: return "dtype must be float16 or bfloat16";
+        case RSFA_E_DTYPE: return "dtype must be float16 or bfloat16 (q, k, v, o), or float16 q, k, o with a float8_e5m2 v";
         case RSFA_E_TILE: return "invalid BLOCK_M/BLOCK_N: powers of two in [16, 512], BLOCK_M*BLOCK_N <= 65536, "
                                  "and BLOCK_N <= BLOCK_M when causal";
         case RSFA_E_ALIGN: return "tensors need a unit last-dim stride, other strides multiple of 8 elements "
@@ -288,7 +324,7 @@ int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype, int32_t
                         int32_t* block_m, int32_t* block_n) {
     if (!block_m || !block_n) return RSFA_E_NULL;
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
-    if (dtype != RSFA_DTYPE_F16 && dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
     const KernelEntry* e = nullptr;
     const int st = resolve(head_dim, causal, dtype, req_block_m, req_block_n, &e);
     if (st != RSFA_OK) return st;
@@ -302,7 +338,7 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     if (!block_m || !block_n) return RSFA_E_NULL;
     if (z < 1 || h < 1 || n_ctx < 1) return RSFA_E_SHAPE;
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
-    if (dtype != RSFA_DTYPE_F16 && dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
     // The cost model is evaluated for a 256-CU MI355X so the answer does not
     // depend on whether a GPU is visible to the caller.
     const KernelEntry* e = nullptr;
@@ -311,6 +347,11 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     *block_m = 32 * e->nw;
     *block_n = e->bn;
     return RSFA_OK;
+}
+
+uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim) {
+    if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim)) return 0;
+    return (uint64_t)(z * h * n_ctx * head_dim) * 2;
 }
 
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32_t block_m) {
@@ -324,14 +365,15 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     if (!a) return RSFA_E_NULL;
     if (a->struct_size != sizeof(rsfa_fwd_args)) return RSFA_E_ABI;
     if (!a->q || !a->k || !a->v || !a->o) return RSFA_E_NULL;
-    if (a->dtype != RSFA_DTYPE_F16 && a->dtype != RSFA_DTYPE_BF16) return RSFA_E_DTYPE;
+    if (!valid_dtype(a->dtype)) return RSFA_E_DTYPE;
+    const bool v8 = a->dtype == RSFA_DTYPE_F16_V8E5M2;
     if (!valid_head_dim(a->head_dim)) return RSFA_E_HEADDIM;
     if (a->z < 1 || a->h < 1 || a->n_ctx < 1 || a->n_ctx > (1 << 30) || a->z * a->h > (1 << 30))
         return RSFA_E_SHAPE;
     int st;
     if ((st = check_tensor(a->q, a->q_stride)) != RSFA_OK) return st;
     if ((st = check_tensor(a->k, a->k_stride)) != RSFA_OK) return st;
-    if ((st = check_tensor(a->v, a->v_stride)) != RSFA_OK) return st;
+    if ((st = check_tensor(a->v, a->v_stride, v8 ? 16 : 8)) != RSFA_OK) return st;
     if ((st = check_tensor(a->o, a->o_stride)) != RSFA_OK) return st;
     if (((uintptr_t)a->lse & 3) != 0) return RSFA_E_ALIGN;
     const bool causal = a->causal != 0;
@@ -375,11 +417,27 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     if (p.c < FLT_MIN) p.c = FLT_MIN;
     p.neg = sc < 0.0f ? 1u : 0u;
 
-    if (split) {
-        const uint64_t need = rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm);
+    // workspace: the fp16 copy of a float8 V first, then the split state
+    const uint64_t v8_bytes = v8 ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
+    if (v8 || split) {
+        const uint64_t need =
+            v8_bytes + (split ? rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm) : 0);
         if (!a->workspace || a->workspace_bytes < need) return RSFA_E_WORKSPACE;
-        if (((uintptr_t)a->workspace & 3) != 0) return RSFA_E_ALIGN;
-        p.state = (float*)a->workspace;
+        if (((uintptr_t)a->workspace & (v8 ? 15 : 3)) != 0) return RSFA_E_ALIGN;
+        if (split) p.state = (float*)((char*)a->workspace + v8_bytes);
+    }
+    if (v8) {
+        uint32_t* wide = (uint32_t*)a->workspace;
+        const int64_t chunks = a->z * a->h * a->n_ctx * (a->head_dim / 16);
+        const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((chunks + 255) / 256, (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(widen_v8, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                           (const uint8_t*)a->v, a->v_stride[0], a->v_stride[1], a->v_stride[2], (int32_t)a->h,
+                           (int32_t)a->n_ctx, (int32_t)a->head_dim, chunks, wide);
+        if (hipGetLastError() != hipSuccess) return RSFA_E_LAUNCH;
+        p.v = wide;
+        p.v_sn = a->head_dim;
+        p.v_sh = a->n_ctx * a->head_dim;
+        p.v_sz = a->h * p.v_sh;
     }
 
     const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE);

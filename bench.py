@@ -32,7 +32,7 @@ METRIC = "FA2 fwd TFLOP/s + % fp16 MFMA peak (causal & non-causal), ms/call"
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 PEAK_HBM_GBS = 8000.0
 
-# name, B, H, S, D, causal, sm_scale, seed
+# name, B, H, S, D, causal, sm_scale, seed[, V dtype]
 CONFIGS = [
     ("C2", 32, 8, 2048, 128, False, 1 / math.sqrt(128), 1236),   # the `value`
     ("C3", 128, 8, 2048, 128, True, 0.5, 1237),
@@ -41,6 +41,8 @@ CONFIGS = [
     ("C4-causal", 64, 8, 1024, 256, True, 1 / 16, 1238),
     ("C5", 4, 16, 8192, 64, True, 1 / 8, 1239),
     ("C1", 2, 8, 1024, 128, True, 0.5, 1235),
+    # the reference's fp8_v branch (flash_attention_forward.py:208-211): fp16 Q, K, O, float8 e5m2 V
+    ("C2-v8e5m2", 32, 8, 2048, 128, False, 1 / math.sqrt(128), 1236, "e5m2"),
 ]
 # HBM bytes per launch of the C2 kernel, from two rocprofv3 --pmc passes
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "fa_fwd_c2_traffic.txt")
@@ -50,20 +52,22 @@ def flops(B, H, S, D, causal):
     return 4.0 * B * H * S * S * D * (0.5 if causal else 1.0)
 
 
-def algo_bytes(B, H, S, D, causal):
-    # Q, K, V read once, O written once (fp16); non-causal attention() also
-    # writes the fp32 row logsumexp M (reference flash_attention_forward.py:400-403)
-    return 2.0 * 4 * B * H * S * D + (0.0 if causal else 4.0 * B * H * S)
+def algo_bytes(B, H, S, D, causal, v_bytes=2):
+    # Q, K, V read once, O written once (fp16; V 1 byte when float8); non-causal
+    # attention() also writes the fp32 row logsumexp M (reference 400-403)
+    return (2.0 * 3 + v_bytes) * B * H * S * D + (0.0 if causal else 4.0 * B * H * S)
 
 
 def time_config(F, torch, cfg, steps, warmup):
-    name, B, H, S, D, causal, scale, seed = cfg
+    name, B, H, S, D, causal, scale, seed = cfg[:8]
+    v8 = len(cfg) > 8 and cfg[8] == "e5m2"
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     shape = (B, H, S, D)
     q = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).half()
     k = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).half()
-    v = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).half()
+    v = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
+    v = v.to(torch.float8_e5m2) if v8 else v.half()
     BM, BN = F.get_tiling(B, H, S, D, causal)
     for _ in range(warmup):
         F.attention(q, k, v, causal, scale, BM, BN)
@@ -85,7 +89,8 @@ def time_config(F, torch, cfg, steps, warmup):
         "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "tiling": [BM, BN],
         "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
         "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
-        "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal) / (ms * 1e-3) / 1e9, 1),
+        "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal, 1 if v8 else 2) / (ms * 1e-3) / 1e9, 1),
+        **({"v_dtype": "float8_e5m2"} if v8 else {}),
     }
 
 

@@ -16,14 +16,18 @@
  *   rsfa_resolve_tiling       -> the (BLOCK_M, BLOCK_N) meta-parameters the
  *                                reference passes to _attn_fwd[grid] (518-519, 606-607)
  *   rsfa_get_num_compute_cores-> get_num_compute_cores(), 19-21
+ *   rsfa_v8_workspace_bytes   -> (no separate counterpart: the size of the
+ *                                fp16 copy of a float8 V, for the fp8_v
+ *                                branch of _attn_fwd_inner, 208-211)
  *   rsfa_strerror             -> (no counterpart: the reference raises Python
  *                                exceptions; codes map to them in the wrapper)
  *
  * Conventions
  *   - All tensor pointers are device pointers owned by the caller; the library
  *     never frees them.  Strides are in elements.  The last (head-dim) stride
- *     of q/k/v/o must be 1, every other stride a multiple of 8 elements and
- *     every base pointer 16-byte aligned (RSFA_E_ALIGN otherwise).
+ *     of q/k/v/o must be 1, every other stride a multiple of 8 elements (16
+ *     for a float8 V) and every base pointer 16-byte aligned (RSFA_E_ALIGN
+ *     otherwise).
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t, NULL = the
  *     null stream).  The call returns after the launch, not after completion.
  *   - Return codes: 0 on success, a negative rsfa_status otherwise.  Invalid
@@ -38,25 +42,33 @@
 extern "C" {
 #endif
 
-#define RSFA_ABI_VERSION 1
+#define RSFA_ABI_VERSION 2
 
 typedef enum rsfa_status {
     RSFA_OK          = 0,
     RSFA_E_NULL      = -1,  /* a required pointer is NULL                      */
     RSFA_E_SHAPE     = -2,  /* Z, H or N_CTX not >= 1, or too large             */
     RSFA_E_HEADDIM   = -3,  /* head_dim not in {16, 32, 64, 128, 256}           */
-    RSFA_E_DTYPE     = -4,  /* dtype not RSFA_DTYPE_F16 / RSFA_DTYPE_BF16       */
+    RSFA_E_DTYPE     = -4,  /* dtype not one of rsfa_dtype                      */
     RSFA_E_TILE      = -5,  /* block_m/block_n invalid (see rsfa_resolve_tiling)*/
     RSFA_E_ALIGN     = -6,  /* stride / alignment contract violated             */
     RSFA_E_DEVICE    = -7,  /* HIP runtime error while querying or preparing    */
     RSFA_E_LAUNCH    = -8,  /* kernel launch failed                             */
     RSFA_E_ABI       = -9,  /* struct_size does not match this library          */
-    RSFA_E_WORKSPACE = -10  /* split mode without a large enough workspace      */
+    RSFA_E_WORKSPACE = -10  /* split mode or a float8 V without a large enough
+                               workspace                                        */
 } rsfa_status;
 
 typedef enum rsfa_dtype {
-    RSFA_DTYPE_F16  = 0,
-    RSFA_DTYPE_BF16 = 1
+    RSFA_DTYPE_F16  = 0,         /* q, k, v, o float16                         */
+    RSFA_DTYPE_BF16 = 1,         /* q, k, v, o bfloat16                        */
+    RSFA_DTYPE_F16_V8E5M2 = 2    /* q, k, o float16; v float8 e5m2 (OCP: sign,
+                                    5 exponent bits, bias 15, 2 mantissa bits).
+                                    P is rounded to e5m2 for P.V and the row
+                                    sums add the unrounded P, as the reference's
+                                    fp8_v branch does (208-211, 217).  The
+                                    library first widens V to fp16 (exactly)
+                                    in `workspace`: see rsfa_v8_workspace_bytes */
 } rsfa_dtype;
 
 /* flags (bit set) */
@@ -77,7 +89,9 @@ typedef struct rsfa_fwd_args {
     float      *lse;          /* optional [Z, H, N_CTX] fp32, natural-log
                                  logsumexp of the scaled scores (the reference's
                                  M = m + ln(l), 400-403); NULL = not written    */
-    void       *workspace;    /* split mode only, see rsfa_split_workspace_bytes */
+    void       *workspace;    /* split mode and/or a float8 V: the fp16 copy of
+                                 V (rsfa_v8_workspace_bytes) first, then the
+                                 split state (rsfa_split_workspace_bytes)      */
     uint64_t    workspace_bytes;
     int64_t     z, h, n_ctx, head_dim;
     int64_t     q_stride[4];  /* element strides of dims (Z, H, N_CTX, D)       */
@@ -100,6 +114,12 @@ int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
  * also keeps the un-normalised accumulator in fp32 instead of fp16 in O). */
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                     int64_t head_dim, int32_t block_m);
+
+/* Bytes of workspace a float8 V (RSFA_DTYPE_F16_V8E5M2) needs: the fp16 copy
+ * of V, contiguous [Z, H, N_CTX, D].  Split mode adds its state after it, at
+ * this offset.  0 for invalid sizes. */
+uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
+                                 int64_t head_dim);
 
 /* Tile search for gfx950 (replaces the lookup table get_tiling, 624-665):
  * writes the (BLOCK_M, BLOCK_N) this library would pick for the shape.

@@ -19,6 +19,22 @@ reference_attention / reference_lse
       * planted mistakes (shifted diagonal, dropped scale, transposed V,
         softmax over the wrong axis) each fail at least one of the above.
 
+round_e5m2 / reference_attention_fp8v / fp8v_error_bound
+    The reference's fp8_v branch (flash_attention_forward.py:208-211, 217,
+    453-456, 466): with V in float8 e5m2, P = exp(S - m) is cast to e5m2 for
+    P.V while the row sum l adds the unrounded P.  round_e5m2 restates the
+    OCP e5m2 format (sign, 5 exponent bits with bias 15, 2 fraction bits,
+    subnormals down to 2^-16, round to nearest even) from its definition.
+    reference_attention_fp8v evaluates the branch with the exact row max (one
+    key tile), fp8v_error_bound bounds any tiling of it: every P element is
+    rounded with relative error <= 2^-3 (normal range) or absolute error
+    <= 2^-17 (subnormal range, in units where the row max is >= 1).
+    Pinned by (tests/test_oracle.py): torch's own float32 -> float8_e5m2
+    conversion on values across every binade, ties and the subnormal range;
+    every finite e5m2 value maps to itself; sm_scale = 0 gives the mean of V
+    exactly; a two-key case (p = 1 and 0.6, 0.6 rounds to 0.625) tells the
+    unrounded row sum (O = 0.625 / 1.6) from a rounded one (0.625 / 1.625).
+
 blockwise_attention
     The reference's tiled algorithm with its rounding points (fp16 P, fp16
     round trip of the unnormalised prefix accumulator, -1e6 additive mask,
@@ -86,6 +102,73 @@ def reference_attention(q, k, v, causal, sm_scale, return_lse=False, heads=None)
         if lse is not None:
             lse = lse.reshape(Z, H, N)
     return (out, lse) if return_lse else out
+
+
+E5M2_MAX = 57344.0  # 1.75 * 2^15, the largest finite e5m2
+
+
+def round_e5m2(x):
+    """Round to the nearest float8 e5m2 value (ties to even), returned as float32.
+
+    e5m2: sign, 5 exponent bits (bias 15), 2 fraction bits.  Normal values
+    1.f x 2^e for e in [-14, 15]; subnormals 0.f x 2^-14 (spacing 2^-16).
+    Magnitudes that round above E5M2_MAX become inf.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    a = np.abs(x).astype(np.float64)
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    e = np.maximum(e, -14.0)  # below 2^-14 the spacing stays 2^-16
+    q = np.exp2(e - 2.0)      # spacing of e5m2 values in the binade of a
+    r = np.round(a / q) * q   # numpy rounds halves to even; a / q is exact
+    r = np.where(r > E5M2_MAX, np.inf, r)
+    r = np.where(np.isinf(a), np.inf, r)
+    return (np.sign(x) * r).astype(np.float32)
+
+
+def _heads_f32(q, k, v, heads):
+    Z, H, N, D = q.shape
+    if heads is None:
+        heads = [(z, h) for z in range(Z) for h in range(H)]
+    pick = lambda t: torch.stack([t[z, h] for z, h in heads]).detach().to("cpu", torch.float32)
+    return pick(q), pick(k), pick(v), heads
+
+
+def _scores_exp(qf, kf, causal, sm_scale):
+    """p = exp(S - rowmax S) (masked keys 0), float64, with S in float32."""
+    s = torch.matmul(qf, kf.transpose(-1, -2)) * float(sm_scale)
+    if causal:
+        s.masked_fill_(causal_mask(s.shape[-1]), float("-inf"))
+    s = s.double()
+    p = torch.exp(s - s.max(dim=-1, keepdim=True).values)
+    return p
+
+
+def reference_attention_fp8v(q, k, v8, causal, sm_scale, heads=None):
+    """The reference's fp8_v branch with the exact row max (a single key
+    tile): O = (e5m2(P) @ V) / sum(P), P = exp(S - max S); [len(heads), N, D]
+    (all heads when ``heads`` is None, then reshaped to [Z, H, N, D])."""
+    qf, kf, vf, hs = _heads_f32(q, k, v8.float(), heads)
+    p = _scores_exp(qf, kf, causal, sm_scale)
+    p8 = torch.from_numpy(round_e5m2(p.float().numpy())).double()
+    out = (torch.matmul(p8, vf.double()) / p.sum(dim=-1, keepdim=True)).float()
+    return out.reshape(q.shape) if heads is None else out
+
+
+def fp8v_error_bound(q, k, v8, causal, sm_scale, heads=None):
+    """Elementwise bound on |O - O_exact| for any tiling of the fp8_v branch,
+    O_exact = softmax(S) V with V's e5m2 values: P rounding (2^-3 relative,
+    2^-17 absolute in the subnormal range), fp32 accumulation, fp16 output."""
+    qf, kf, vf, hs = _heads_f32(q, k, v8.float(), heads)
+    p = _scores_exp(qf, kf, causal, sm_scale)
+    av = vf.double().abs()
+    l = p.sum(dim=-1, keepdim=True)
+    vis = (p > 0).double() if causal else torch.ones_like(p)
+    exact = torch.matmul(p, vf.double()) / l
+    b = (0.126 * torch.matmul(p, av) + 2.0 ** -17 * torch.matmul(vis, av)) / l
+    b = b + 2.0 ** -10 * exact.abs() + 1e-4
+    b = b.float()
+    return b.reshape(q.shape) if heads is None else b
 
 
 def brute_force_attention_f64(q, k, v, causal, sm_scale):

@@ -1,0 +1,113 @@
+"""GPU parity of the float8 e5m2 V path (the reference's fp8_v branch,
+flash_attention_forward.py:208-211, 217, 453-456, 466) against the oracle:
+known answers that pin the e5m2 rounding of P and the unrounded row sum, the
+provable per-element bound for random inputs, strided V and the split mode."""
+import numpy as np
+import pytest
+import torch
+
+from ascend_rsfa import flash_attention_forward as faf
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v8, causal, scale, **kw):
+    print(f"fp8v: shape={tuple(q.shape)} causal={causal} scale={scale} {kw}", flush=True)
+    o = faf.forward(q.cuda(), k.cuda(), v8.cuda(), causal, scale, **kw)
+    torch.cuda.synchronize()
+    return o.float().cpu()
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_two_key_case_rounds_p_and_sums_it_unrounded(d, causal):
+    q = torch.zeros(1, 1, 2, d)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 1, 2, d)
+    k[0, 0, 1, 0] = float(np.log(0.6))
+    v = torch.zeros(1, 1, 2, d)
+    v[0, 0, 1] = 1.0
+    q, k, v8 = q.half(), k.half(), v.to(torch.float8_e5m2)
+    p1 = float(np.exp(float(k[0, 0, 1, 0])))
+    o = _run(q, k, v8, causal, 1.0)
+    want = 0.625 / (1.0 + p1)  # e5m2(0.6) = 0.625 over the unrounded sum 1.6
+    assert abs(o[0, 0, 1, 0].item() - want) < 1e-3
+    assert abs(o[0, 0, 1, 0].item() - 0.625 / 1.625) > 3e-3  # not the rounded sum
+    assert abs(o[0, 0, 0, 0].item() - (0.0 if causal else want)) < 1e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_zero_scale_gives_the_mean_of_v(causal):
+    q, k, v = A.make_inputs(2, 3, 200, 64, seed=5)
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, causal, 0.0)
+    ref = A.reference_attention_fp8v(q, k, v8, causal, 0.0)
+    assert (o - ref).abs().max().item() < 2e-3
+
+
+CASES = [  # Z, H, N, D, causal, sm_scale
+    (2, 4, 300, 64, False, 0.125),
+    (1, 4, 512, 128, True, 0.08),
+    (2, 2, 256, 256, False, 0.0625),
+    (1, 2, 1000, 128, True, 0.5),
+    (2, 2, 333, 32, True, 0.2),
+    (1, 3, 130, 16, False, 0.25),
+    (1, 8, 2048, 128, False, 1 / np.sqrt(128)),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_random_inputs_within_the_rounding_bound(case):
+    Z, H, N, D, causal, scale = case
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + D)
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, causal, scale)
+    heads = [(0, 0), (Z - 1, H - 1)]
+    exact = A.reference_attention(q, k, v8.float(), causal, scale, heads=heads)
+    bound = A.fp8v_error_bound(q, k, v8, causal, scale, heads=heads)
+    got = torch.stack([o[z, h] for z, h in heads])
+    assert torch.isfinite(got).all()
+    excess = ((got - exact).abs() - bound).max().item()
+    assert excess <= 0, f"outside the bound by {excess}"
+
+
+def test_p_rounding_is_active():
+    q, k, v = A.make_inputs(1, 2, 512, 64, seed=9)
+    v8 = v.to(torch.float8_e5m2)
+    o8 = _run(q, k, v8, False, 0.05)
+    o16 = _run(q, k, v8.half(), False, 0.05)  # same V values, P rounded to fp16 instead
+    assert (o8 - o16).abs().max().item() > 1e-3
+
+
+def test_strided_float8_v_matches_contiguous():
+    q, k, v = A.make_inputs(2, 3, 160, 64, seed=13)
+    store = v.permute(0, 2, 1, 3).contiguous().to(torch.float8_e5m2)  # [Z, N, H, D] storage
+    v_view = store.permute(0, 2, 1, 3)  # [Z, H, N, D] view, strides (N*H*D, D, H*D, 1)
+    assert not v_view.is_contiguous() and all(s % 16 == 0 for s in v_view.stride()[:3])
+    a = _run(q, k, v_view.cuda(), True, 0.3)
+    b = _run(q, k, v_view.contiguous(), True, 0.3)
+    assert torch.equal(a, b)
+
+
+def test_split_mode_with_float8_v():
+    q, k, v = A.make_inputs(1, 4, 700, 128, seed=17)
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, True, 0.25, split=True)
+    heads = [(0, 0), (0, 3)]
+    exact = A.reference_attention(q, k, v8.float(), True, 0.25, heads=heads)
+    bound = A.fp8v_error_bound(q, k, v8, True, 0.25, heads=heads)
+    got = torch.stack([o[z, h] for z, h in heads])
+    assert ((got - exact).abs() <= bound).all()
+
+
+def test_reference_entry_point_accepts_float8_v():
+    q, k, v = A.make_inputs(1, 2, 256, 64, seed=21)
+    v8 = v.to(torch.float8_e5m2)
+    print("fp8v: attention() entry point", flush=True)
+    o = faf.attention(q.cuda(), k.cuda(), v8.cuda(), False, 0.125, *faf.get_tiling(1, 2, 256, 64, False))
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16 and o.shape == q.shape
+    exact = A.reference_attention(q, k, v8.float(), False, 0.125)
+    bound = A.fp8v_error_bound(q, k, v8, False, 0.125)
+    assert ((o.float().cpu() - exact).abs() <= bound).all()

@@ -123,6 +123,24 @@ def test_split_workspace_bytes_matches_reference_state_shape():
     assert lib.rsfa_split_workspace_bytes(0, 3, 100, 64, 64) == 0
 
 
+def test_v8_workspace_bytes_is_the_fp16_copy_of_v():
+    lib = _native.lib()
+    assert lib.rsfa_v8_workspace_bytes(32, 8, 2048, 128) == 32 * 8 * 2048 * 128 * 2
+    assert lib.rsfa_v8_workspace_bytes(1, 1, 17, 16) == 17 * 16 * 2
+    assert lib.rsfa_v8_workspace_bytes(1, 1, 17, 48) == 0
+    assert lib.rsfa_v8_workspace_bytes(0, 1, 17, 64) == 0
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_float8_v_dtype_has_the_fp16_tilings(causal):
+    lib = _native.lib()
+    for shape in [(32, 8, 2048, 128), (4, 16, 8192, 64), (64, 8, 1024, 256), (2, 8, 1024, 16)]:
+        assert _tiling(*shape, causal, _native.DTYPE_F16_V8E5M2) == _tiling(*shape, causal)
+    bm, bn = ctypes.c_int32(), ctypes.c_int32()
+    assert lib.rsfa_resolve_tiling(128, causal, _native.DTYPE_F16_V8E5M2, 128, 64,
+                                   ctypes.byref(bm), ctypes.byref(bn)) == 0
+
+
 def _valid_args(**over):
     a = _native.FwdArgs()
     a.struct_size = ctypes.sizeof(_native.FwdArgs)
@@ -155,6 +173,9 @@ def _valid_args(**over):
     (dict(v_stride=[3 * 128 * 64, 128 * 64, 64, 2]), _native.E_ALIGN),
     (dict(q_stride=[3 * 128 * 64, 128 * 64, 60, 1]), _native.E_ALIGN),
     (dict(lse=0x1002), _native.E_ALIGN),
+    (dict(dtype=3), _native.E_DTYPE),
+    # a float8 V needs 16-byte rows: outer strides a multiple of 16 elements
+    (dict(dtype=_native.DTYPE_F16_V8E5M2, v_stride=[3 * 128 * 72, 128 * 72, 72, 1]), _native.E_ALIGN),
 ])
 def test_attention_fwd_rejects_invalid_arguments(over, code):
     lib = _native.lib()
