@@ -180,7 +180,7 @@ __device__ __forceinline__ Queue make_queue(const FwdParams& p) {
 __device__ __forceinline__ float swap_max(float x) {
     // {x[l%32], x[l%32 + 32]} in some order for every lane l
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float swap_sum(float x) {
@@ -314,10 +314,12 @@ __device__ __forceinline__ void wait_loads_and_sync() {
 }
 
 // Whether an instantiation runs the ping-pong schedule (8-wave workgroups,
-// three K/V buffers within the 160 KB of LDS of a CU; head dims up to 128,
-// since at 256 the O^T and Q^T registers leave too few for the schedule).
-constexpr bool uses_pingpong(int d, int bn, int nw, int mode) {
-    return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && d <= 128 &&
+// three K/V buffers within the 160 KB of LDS of a CU).  At D = 256 (32-key
+// tiles) O^T and Q^T take 192 of the 256 VGPRs: the loop still fits, a few
+// loop-invariant values spill to scratch outside it; it runs non-causal only
+// (measured +2 % there, -2 to +1 % causal).
+constexpr bool uses_pingpong(int d, int bn, int nw, bool causal, int mode) {
+    return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && (d <= 128 || (d == 256 && !causal)) &&
            3 * (2 * bn * (d < 32 ? 32 : d) * 2) <= 160 * 1024 - 64;
 }
 
@@ -348,7 +350,7 @@ fa_fwd_kernel(FwdParams p) {
     // tiles every row of the workgroup sees unmasked run with waves 4-7 one
     // phase behind waves 0-3, so one wave of each SIMD runs its softmax (VALU)
     // while the other runs its matrix products.  K/V are triple buffered.
-    constexpr bool PP = uses_pingpong(D, BN, NW, MODE);
+    constexpr bool PP = uses_pingpong(D, BN, NW, CAUSAL, MODE);
     constexpr int NBUF = PP ? 3 : 2;
 
     __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
@@ -612,7 +614,9 @@ fa_fwd_kernel(FwdParams p) {
             }
         };
         // Row max of the tile folded into m_use (rescaling O and l when it
-        // moves); returns the value to subtract before exp2.
+        // moves); returns the value to subtract before exp2.  NaN-propagating
+        // (v_maximum3_f32) as the reference's max is (flash_attention_forward.py:
+        // 200-203), which also spares the operand canonicalisation of maxNum.
         auto softmax_max = [&](f32x16 (&sacc)[NKT], auto masked) {
             constexpr bool MASK = decltype(masked)::value;
             float mx = sacc[0][0];
@@ -620,7 +624,7 @@ fa_fwd_kernel(FwdParams p) {
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if (kt + r > 0) mx = fmaxf(mx, sacc[kt][r]);
+                    if (kt + r > 0) mx = __builtin_elementwise_maximum(mx, sacc[kt][r]);
             mx = swap_max(mx);
             const float m_tile = mx * c;
             const bool need = m_tile > m_use + RESCALE_SLACK;
@@ -893,40 +897,48 @@ fa_fwd_kernel(FwdParams p) {
             }
         }
         const float inv = (MODE == MODE_PREFIX) ? (lt > 0.0f ? 1.0f / lt : 0.0f) : 1.0f / lt;
-        // O leaves through LDS when the workgroup's rows fit there: in the
-        // accumulator layout a lane holds 8 bytes of a row per (d, a), so a
-        // direct store instruction writes 32 rows x 16 bytes, and a CU needs
-        // ~64 cycles per such instruction (measured: the second group of
-        // waves waited ~4k cycles per task behind the first group's stores);
-        // staged row-major, each store instruction writes whole 16-byte
-        // chunks of 64 / (D / 8) consecutive rows (+2.5 to +3.6 % on C2, B=128,
-        // C3 and D=64).  D = 256 tiles do not fit and store directly.
-        constexpr int OROW = 2 * D + 16;  // bytes per staged row (16-byte pad)
-        constexpr bool OSTAGE = NW * 32 * OROW <= NBUF * BUF;
+        // O leaves through LDS: in the accumulator layout a lane holds 8 bytes
+        // of a row per (d, a), so a direct store instruction writes 32 rows x
+        // 16 bytes, and a CU needs ~64 cycles per such instruction (measured:
+        // the second group of waves waited ~4k cycles per task behind the
+        // first group's stores); staged row-major, each store instruction
+        // writes whole 16-byte chunks of 64 / (OCOLS / 8) consecutive rows
+        // (+2.5 to +3.6 % on C2, B=128, C3 and D=64).  OCOLS columns of the
+        // workgroup's rows go through the K/V buffers per round: all D when
+        // they fit, else half or a quarter of them (D = 256).
+        constexpr int OCOLS = NW * 32 * (2 * D + 16) <= NBUF * BUF ? D
+                              : NW * 32 * (D + 16) <= NBUF * BUF ? D / 2 : D / 4;
+        constexpr int OROW = 2 * OCOLS + 16;  // bytes per staged row (16-byte pad)
+        constexpr bool OSTAGE = NW * 32 * OROW <= NBUF * BUF && OCOLS >= 16;
         if constexpr (OSTAGE) {
             __syncthreads();  // every wave is done with the K/V tiles
+            // a wave's own region: its reads of one round precede (in LDS
+            // order) its writes of the next, so rounds need no barrier
             RSFA_LDS char* const ow = smem + wave * (32 * OROW);
-#pragma unroll
-            for (int d = 0; d < DT; ++d)
-#pragma unroll
-                for (int a = 0; a < 4; ++a) {
-                    const int col = 32 * d + 8 * a + 4 * hh;
-                    if (col < D) {
-                        x4 v4;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) v4[e] = (elem)(o[d][4 * a + e] * inv);
-                        *(RSFA_LDS x4*)(ow + l32 * OROW + col * 2) = v4;
-                    }
-                }
-            constexpr int CH = D / 8;     // 16-byte chunks per row
-            constexpr int RPI = 64 / CH;  // rows per store instruction
+            constexpr int CH = OCOLS / 8;  // 16-byte chunks per staged row
+            constexpr int RPI = 64 / CH;   // rows per store instruction
             const int rr = lane / CH, cc = (lane % CH) * 8;
             const int row0 = m0 + wave * 32;
 #pragma unroll
-            for (int it = 0; it < 32 / RPI; ++it) {
-                const int r = it * RPI + rr;
-                const x8 v = *(const RSFA_LDS x8*)(ow + r * OROW + cc * 2);
-                if (row0 + r < n) *(x8*)(ob + (int64_t)(row0 + r) * p.o_sm + cc) = v;
+            for (int hf = 0; hf < D / OCOLS; ++hf) {
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) {
+                        const int col = 32 * d + 8 * a + 4 * hh;
+                        if (col < D && col / OCOLS == hf) {
+                            x4 v4;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v4[e] = (elem)(o[d][4 * a + e] * inv);
+                            *(RSFA_LDS x4*)(ow + l32 * OROW + (col - hf * OCOLS) * 2) = v4;
+                        }
+                    }
+#pragma unroll
+                for (int it = 0; it < 32 / RPI; ++it) {
+                    const int r = it * RPI + rr;
+                    const x8 v = *(const RSFA_LDS x8*)(ow + r * OROW + cc * 2);
+                    if (row0 + r < n) *(x8*)(ob + (int64_t)(row0 + r) * p.o_sm + hf * OCOLS + cc) = v;
+                }
             }
             if (MODE != MODE_PREFIX && p.lse && hh == 0 && qrow < n)
                 p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;

@@ -34,9 +34,9 @@ KernelList kernels_d256();
 
 // One tile configuration: non-causal fused, causal fused, causal prefix, causal diagonal.
 #define RSFA_TILE_ENTRIES(T, DTYPE, D, BN, NW, OCC)                                                  \
-    {DTYPE, D, BN, NW, 0, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, MODE_FUSED),                          \
+    {DTYPE, D, BN, NW, 0, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, false, MODE_FUSED),                   \
      (const void*)&fa_fwd_kernel<T, D, BN, NW, false, MODE_FUSED, OCC>},                                  \
-    {DTYPE, D, BN, NW, 1, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, MODE_FUSED),                          \
+    {DTYPE, D, BN, NW, 1, MODE_FUSED, OCC, uses_pingpong(D, BN, NW, true, MODE_FUSED),                    \
      (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_FUSED, OCC>},                                   \
     {DTYPE, D, BN, NW, 1, MODE_PREFIX, OCC, 0, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_PREFIX, OCC>}, \
     {DTYPE, D, BN, NW, 1, MODE_DIAG, OCC, 0, (const void*)&fa_fwd_kernel<T, D, BN, NW, true, MODE_DIAG, OCC>}
