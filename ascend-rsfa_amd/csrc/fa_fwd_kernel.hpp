@@ -352,6 +352,12 @@ fa_fwd_kernel(FwdParams p) {
     // while the other runs its matrix products.  K/V are triple buffered.
     constexpr bool PP = uses_pingpong(D, BN, NW, CAUSAL, MODE);
     constexpr int NBUF = PP ? 3 : 2;
+    // Causal ping-pong tiles also cover the diagonal key tiles of a whole
+    // query block: the first S^T MFMA of each 32-key sub-tile accumulates onto
+    // a per-wave bias block (0 below the wave's rows, -inf above, triangular
+    // on its diagonal), so masking costs no VALU work per score.  Two
+    // sub-tiles per tile (32 VGPRs).
+    constexpr bool DIAG_PP = CAUSAL && PP && NKT <= 2;
 
     __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
     __shared__ int s_ticket;
@@ -502,6 +508,9 @@ fa_fwd_kernel(FwdParams p) {
         // The first loads go out before the Q loads, so their latencies overlap.
         int jpp = j0;
         if constexpr (PP) jpp = min(j1, (CAUSAL ? m0 : n) / BN);
+        if constexpr (DIAG_PP) {
+            if (m0 + BM <= n) jpp = j1;  // the diagonal tiles too (whole tiles only)
+        }
         if (jpp > j0) {
             load_k(j0);
             load_v(j0);
@@ -530,6 +539,21 @@ fa_fwd_kernel(FwdParams p) {
             for (int r = 0; r < 16; ++r) o[d][r] = 0.0f;
         float m_use = -INFINITY;  // running max (exp2 domain) of this lane's query row
         float l_sum = 0.0f;       // this lane's half of the row sum
+        // Bias blocks of the diagonal ping-pong tiles: sub-tile kt of tile tt
+        // lies below (<0), on (0) or above (>0) this wave's 32 rows.
+        f32x16 cb[DIAG_PP ? NKT : 1];
+        auto cb_rel = [&](int tt, int kt) { return tt * NKT + kt - (m0 / 32 + wave); };
+        auto cb_fill = [&](int kt, int rel) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int kk = 8 * (i >> 2) + 4 * hh + (i & 3);  // key of register i in the sub-tile
+                cb[kt][i] = rel < 0 ? 0.0f : (rel > 0 || kk > l32) ? -INFINITY : 0.0f;
+            }
+        };
+        if constexpr (DIAG_PP) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) cb_fill(kt, cb_rel(j0, kt));
+        }
 
         const int srow = bh * p.nmb * BM + m0 + wave * 32 + l32;  // split-state row
         if (MODE == MODE_DIAG) {
@@ -587,7 +611,8 @@ fa_fwd_kernel(FwdParams p) {
                     constexpr int ss = i / NKT, kt = i % NKT;
                     constexpr int ahead = (NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1);
                     lgkm_wait<ahead>(ring[i % NB]);
-                    sacc[kt] = T::mfma(__builtin_bit_cast(x8, ring[i % NB]), qf[ss], ss == 0 ? zero : sacc[kt]);
+                    sacc[kt] = T::mfma(__builtin_bit_cast(x8, ring[i % NB]), qf[ss],
+                                       ss == 0 ? (DIAG_PP ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
                     if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
                 });
             } else {
@@ -807,7 +832,8 @@ fa_fwd_kernel(FwdParams p) {
                         } else {
                             constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
                             lgkm_wait<N>(kr[i % XNB]);
-                            sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss], ss == 0 ? zero : sacc[kt]);
+                            sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss],
+                                               ss == 0 ? (DIAG_PP ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
                         }
                         if constexpr (m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
                         // load q of NDMA at op D0 + q * DSTEP (q < NDMA: the wave's K
@@ -842,6 +868,14 @@ fa_fwd_kernel(FwdParams p) {
                     x8 pk[NKT][2];
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
+                    if constexpr (DIAG_PP) {
+                        // bias of tile t+1 where it changes: onto the diagonal, or past it
+#pragma unroll
+                        for (int kt = 0; kt < NKT; ++kt) {
+                            const int rel = cb_rel(t + 1, kt);
+                            if (rel == 0 || (rel > 0 && rel - NKT <= 0)) cb_fill(kt, rel);
+                        }
+                    }
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc);
