@@ -814,14 +814,17 @@ fa_fwd_kernel(FwdParams p) {
                 // X phase of PV(tv) and, when M > NPV, QK(tv + 1); with tl >= 0 it
                 // first waits for the loads of the previous X phase, then loads
                 // K_{tl+1} (if tl + 1 < jpp) and V_tl (if tl < jpp).
+                // LDS byte addresses of the buffers of tiles tv, tv + 1, tv + 2
+                // (rotated once per tile instead of computing jj % NBUF)
+                uint32_t b_tv = smem_addr + bofs(j0), b_t1 = smem_addr + bofs(j0 + 1), b_t2 = smem_addr + bofs(j0 + 2);
                 auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT]) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
                     static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
-                    xa[0] = smem_addr + bofs(tv) + TILE + voff[0];
-                    xa[1] = smem_addr + bofs(tv) + TILE + voff[1];
-                    xa[2] = smem_addr + bofs(tv + 1) + koff[0];
-                    xa[3] = smem_addr + bofs(tv + 1) + koff[1];
+                    xa[0] = b_tv + TILE + voff[0];
+                    xa[1] = b_tv + TILE + voff[1];
+                    xa[2] = b_t1 + koff[0];
+                    xa[3] = b_t1 + koff[1];
                     static_for<(XPF < M ? XPF : M)>(x_issue);
                     const f32x16 zero = {};
                     static_for<M>([&](auto mc) {
@@ -846,10 +849,11 @@ fa_fwd_kernel(FwdParams p) {
                             static_assert(q < NDMA, "load slot past the wave's slices");
                             if (tl >= 0) {
                                 if constexpr (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                                // tl = tv + 2: K_{tv+3} into the buffer of tile tv, V_{tv+2}
                                 if constexpr (q < NSL) {
-                                    if (tl + 1 < jpp) dma_k(tl + 1, q);
+                                    if (tl + 1 < jpp) pp_dma(kh, p.k_sn, kgo, tl + 1, b_tv, q);
                                 } else {
-                                    if (tl < jpp) dma_v(tl, q - NSL);
+                                    if (tl < jpp) pp_dma(vh, p.v_sn, vgo, tl, b_t2 + TILE, q - NSL);
                                 }
                             }
                         }
@@ -882,6 +886,10 @@ fa_fwd_kernel(FwdParams p) {
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc);
+                    const uint32_t b_old = b_tv;
+                    b_tv = b_t1;
+                    b_t1 = b_t2;
+                    b_t2 = b_old;
                 }
                 {
                     phase_barrier();  // Y of the last tile
