@@ -8,8 +8,10 @@
 //   One task = (batch b, head h, query block mb) of BM = 32*NW query rows.
 //   A workgroup of NW wave64s runs tasks from a persistent queue; wave w owns
 //   the 32 query rows [mb*BM + 32w, +32).  K and V stream through LDS in tiles
-//   of BN keys, double buffered: tile j+1 is fetched with direct global->LDS
-//   loads (global_load_lds_dwordx4) while tile j is computed.
+//   of BN keys with direct global->LDS loads (global_load_lds_dwordx4): double
+//   buffered in the one-phase body (tile j+1 arrives while tile j is computed),
+//   triple buffered in the two-phase ping-pong schedule of 8-wave workgroups,
+//   where one wave of each SIMD runs its MFMAs while the other runs its softmax.
 //
 // Contractions (v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulation)
 //   S^T = K Q^T : A = K rows from LDS (ds_read_b128), B = Q^T kept in VGPRs for
