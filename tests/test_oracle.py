@@ -212,3 +212,24 @@ def test_c_half_conversions_match_numpy():
     bf = np.array([lib.rsfa_oracle_f32_to_bf16(float(x)) for x in xs[:2000]], dtype=np.uint16)
     want_bf = torch.from_numpy(xs[:2000]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(bf, want_bf)
+
+
+def _fingerprints():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "input_fingerprints.json")
+    with open(path) as f:
+        return json.load(f)["configs"]
+
+
+def test_input_fingerprints_cover_the_baseline_configs_and_match_c1():
+    fp = _fingerprints()
+    assert sorted(fp) == ["C1", "C2", "C3", "C4", "C5"]
+    c1 = fp["C1"]
+    q, k, v = A.make_inputs(*c1["shape"], c1["seed"])
+    assert A.fingerprint(q, k, v) == c1["sha256"]
+    # a different seed, or k and v drawn in the other order, changes it
+    q2, k2, v2 = A.make_inputs(*c1["shape"], c1["seed"] + 1)
+    assert A.fingerprint(q2, k2, v2) != c1["sha256"]
+    assert A.fingerprint(q, v, k) != c1["sha256"]
