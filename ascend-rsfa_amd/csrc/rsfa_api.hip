@@ -304,7 +304,9 @@ const char* rsfa_strerror(int status) {
         case RSFA_E_DEVICE: return "HIP runtime error while preparing the device";
         case RSFA_E_LAUNCH: return "kernel launch failed";
         case RSFA_E_ABI: return "rsfa_fwd_args.struct_size does not match this library";
-        case RSFA_E_WORKSPACE: return "causal split mode needs a workspace of rsfa_split_workspace_bytes()";
+        case RSFA_E_WORKSPACE:
+            return "workspace missing or smaller than rsfa_v8_workspace_bytes() (float8 V) plus "
+                   "rsfa_split_workspace_bytes() (causal split mode)";
         default: return "unknown rsfa status";
     }
 }

@@ -111,3 +111,50 @@ def test_reference_entry_point_accepts_float8_v():
     exact = A.reference_attention(q, k, v8.float(), False, 0.125)
     bound = A.fp8v_error_bound(q, k, v8, False, 0.125)
     assert ((o.float().cpu() - exact).abs() <= bound).all()
+
+
+def _raw_args(q, k, v, o, dtype_code, causal=False, flags=0, ws=0, ws_bytes=0):
+    import ctypes
+
+    from ascend_rsfa import _native
+
+    a = _native.FwdArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.dtype = dtype_code
+    a.q, a.k, a.v, a.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    a.z, a.h, a.n_ctx, a.head_dim = q.shape
+    for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", o)):
+        getattr(a, name)[:] = list(t.stride())
+    a.sm_scale, a.causal, a.flags = 0.1, int(causal), flags
+    a.workspace, a.workspace_bytes = ws, ws_bytes
+    return a
+
+
+def test_workspace_size_and_alignment_are_checked_before_any_launch():
+    import ctypes
+
+    from ascend_rsfa import _native
+
+    lib = _native.lib()
+    q, k, v = (t.cuda() for t in A.make_inputs(1, 2, 128, 64, seed=23))
+    v8, o = v.to(torch.float8_e5m2), torch.empty_like(q)
+    need = int(lib.rsfa_v8_workspace_bytes(1, 2, 128, 64))
+    ws = torch.empty(need // 4 + 16, dtype=torch.float32, device="cuda")
+    run = lambda a: lib.rsfa_attention_fwd(ctypes.byref(a), None)  # noqa: E731
+    print("workspace checks", flush=True)
+    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2)) == _native.E_WORKSPACE
+    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, ws=ws.data_ptr(), ws_bytes=need - 16)) == \
+        _native.E_WORKSPACE
+    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, ws=ws.data_ptr() + 4, ws_bytes=need)) == \
+        _native.E_ALIGN
+    # causal split: the state after the float8 V copy, both counted
+    split = int(lib.rsfa_split_workspace_bytes(1, 2, 128, 64, 128))
+    assert run(_raw_args(q, k, q, o, 0, causal=True, flags=_native.FLAG_CAUSAL_SPLIT)) == _native.E_WORKSPACE
+    big = torch.empty((need + split) // 4 + 16, dtype=torch.float32, device="cuda")
+    a = _raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, causal=True, flags=_native.FLAG_CAUSAL_SPLIT,
+                  ws=big.data_ptr(), ws_bytes=need + split - 4)
+    a.block_m, a.block_n = 128, 64
+    assert run(a) == _native.E_WORKSPACE
+    msg = lib.rsfa_strerror(_native.E_WORKSPACE).decode()
+    assert "rsfa_v8_workspace_bytes" in msg and "rsfa_split_workspace_bytes" in msg
+    torch.cuda.synchronize()
