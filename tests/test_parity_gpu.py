@@ -296,3 +296,35 @@ def test_d256_epilogue_column_rounds(causal, N):
         out = torch.full_like(qd, float("nan"))
         F.forward(qd, kd, vd, causal, 1 / 16, bm, bn, out=out)
         _assert_close(out, A.reference_attention(q, k, v, causal, 1 / 16), f"D=256 ({bm},{bn}) N={N}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_long_sequence_few_heads(causal):
+    """A 16384-key sequence over two heads: 256 key tiles per task, few tasks
+    (small-grid tiles), the longest causal rows."""
+    Z, H, N, D = 1, 2, 16384, 64
+    q, k, v = A.make_inputs(Z, H, N, D, seed=51)
+    qd, kd, vd = _to_gpu(q, k, v)
+    print(f"long sequence N={N} causal={causal}", flush=True)
+    out = F.forward(qd, kd, vd, causal, 0.125)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    _assert_close(out[0, 1:2], A.reference_attention(q[:, 1:2], k[:, 1:2], v[:, 1:2], causal, 0.125),
+                  f"N={N} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_many_heads_short_rows(causal):
+    """65536 heads of 17 rows: one partial query block per head, tens of
+    thousands of tasks through the queues."""
+    Z, H, N, D = 2048, 32, 17, 128
+    q, k, v = A.make_inputs(Z, H, N, D, seed=52)
+    qd, kd, vd = _to_gpu(q, k, v)
+    print(f"many heads Z={Z} H={H} N={N} causal={causal}", flush=True)
+    out = torch.full_like(qd, float("nan"))
+    F.forward(qd, kd, vd, causal, 0.2, out=out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    heads = [(0, 0), (1023, 17), (Z - 1, H - 1)]
+    ref = A.reference_attention(q, k, v, causal, 0.2, heads=heads)
+    _assert_close(torch.stack([out[z, h] for z, h in heads]), ref, "many heads")
