@@ -254,20 +254,20 @@ int check_tensor(const void* ptr, const int64_t st[4], int mult = 8) {
 // Widens a float8 e5m2 V [Z, H, N, D] (strided, unit head-dim stride) into a
 // contiguous fp16 copy.  An e5m2 byte is the high byte of the fp16 of the same
 // value (same sign, exponent bias 15, two leading mantissa bits), so the copy
-// is exact.  One thread per 16 input bytes, grid-stride.
+// is exact.  One thread per 16 input bytes: x indexes the 16-byte chunks of a
+// head (a row holds 2^lcpr of them, so no division per chunk), y strides over
+// the heads.
 __global__ void __launch_bounds__(256) widen_v8(const uint8_t* __restrict__ v, int64_t sz, int64_t sh,
-                                                int64_t sn, int32_t h, int32_t n, int32_t d,
-                                                int64_t chunks, uint32_t* __restrict__ out) {
-    const int cpr = d / 16;  // 16-byte chunks per row
-    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < chunks;
-         c += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = c / cpr;  // (z * h + hh) * n + m
-        const int ch = (int)(c - row * cpr);
-        const int64_t bh = row / n;
-        const int m = (int)(row - bh * n);
-        const int64_t z = bh / h;
-        const int hh = (int)(bh - z * h);
-        const uint4 w = *(const uint4*)(v + z * sz + hh * sh + (int64_t)m * sn + ch * 16);
+                                                int64_t sn, int32_t h, int32_t nh, int32_t lcpr,
+                                                int64_t per_head, uint32_t* __restrict__ out) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // chunk inside the head
+    if (c >= per_head) return;
+    const int64_t m = c >> lcpr;
+    const int ch = (int)(c & ((1 << lcpr) - 1));
+    for (int bh = blockIdx.y; bh < nh; bh += gridDim.y) {
+        const int z = bh / h;
+        const int hh = bh - z * h;
+        const uint4 w = *(const uint4*)(v + z * sz + hh * sh + m * sn + ch * 16);
         const uint32_t in[4] = {w.x, w.y, w.z, w.w};
         uint32_t o[8];
 #pragma unroll
@@ -275,7 +275,7 @@ __global__ void __launch_bounds__(256) widen_v8(const uint8_t* __restrict__ v, i
             o[2 * i] = ((in[i] << 8) & 0xFF00u) | ((in[i] << 16) & 0xFF000000u);
             o[2 * i + 1] = ((in[i] >> 8) & 0xFF00u) | (in[i] & 0xFF000000u);
         }
-        uint4* dst = (uint4*)(out + c * 8);
+        uint4* dst = (uint4*)(out + ((int64_t)bh * per_head + c) * 8);
         dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
         dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
     }
@@ -430,11 +430,13 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     }
     if (v8) {
         uint32_t* wide = (uint32_t*)a->workspace;
-        const int64_t chunks = a->z * a->h * a->n_ctx * (a->head_dim / 16);
-        const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((chunks + 255) / 256, (int64_t)ds->num_cus * 8));
-        hipLaunchKernelGGL(widen_v8, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                           (const uint8_t*)a->v, a->v_stride[0], a->v_stride[1], a->v_stride[2], (int32_t)a->h,
-                           (int32_t)a->n_ctx, (int32_t)a->head_dim, chunks, wide);
+        const int lcpr = a->head_dim == 16 ? 0 : a->head_dim == 32 ? 1 : a->head_dim == 64 ? 2
+                         : a->head_dim == 128 ? 3 : 4;  // log2 of the 16-byte chunks per row
+        const int64_t per_head = a->n_ctx << lcpr;
+        const int32_t nh = (int32_t)(a->z * a->h);
+        const dim3 grid((unsigned)((per_head + 255) / 256), (unsigned)std::min<int64_t>(nh, 65535));
+        hipLaunchKernelGGL(widen_v8, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a->v,
+                           a->v_stride[0], a->v_stride[1], a->v_stride[2], (int32_t)a->h, nh, lcpr, per_head, wide);
         if (hipGetLastError() != hipSuccess) return RSFA_E_LAUNCH;
         p.v = wide;
         p.v_sn = a->head_dim;
