@@ -9,7 +9,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "librsfa.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # rsfa_status
 OK = 0
@@ -32,6 +32,7 @@ DTYPE_F16_V8E5M2 = 2  # q, k, o float16; v float8_e5m2
 # flags
 FLAG_STATIC_SCHEDULE = 0x1
 FLAG_CAUSAL_SPLIT = 0x2
+FLAG_EXACT_TILE = 0x4
 
 # Every symbol include/rsfa.h declares, with (restype, argtypes).
 _I64 = ctypes.c_int64

@@ -30,20 +30,44 @@ workspace first (exact: an e5m2 byte is the high byte of that fp16).
 Behaviour beyond the reference (documented, deliberate):
 
 * ``BM``/``BN`` keep the reference's meaning (query rows per program, keys per
-  inner tile) and its validity rules; gfx950 runs them on the nearest compiled
-  tile shape (``resolve_tiling``).  Causal calls with ``BN > BM``, which give
-  NaN in the reference (benchmarks/run_correctness_test.py:24-25), raise
-  ``ValueError`` instead.
+  inner tile) and its validity rules, and are a tuning hint as they are in the
+  reference: the tile ``get_tiling`` picks for the shape runs, since values
+  tuned for Ascend's unified buffer say nothing about gfx950
+  (``forward(..., exact_tile=True)`` runs the nearest compiled tile instead).
+  Causal calls with ``BN > BM``, which give NaN in the reference
+  (benchmarks/run_correctness_test.py:24-25), raise ``ValueError`` instead.
 * Any ``N_CTX >= 1`` works (the reference has no load masks, so it needs
   ``N_CTX`` divisible by its tiles).
 * Per-tensor strides are honoured as long as the head dim is unit-stride; other
   layouts are copied to contiguous first.
 """
 import ctypes
+import importlib
+import os
+import sys
 
 import torch
 
-from . import _native
+
+def _package_module(name):
+    """``ascend_rsfa.<name>``, whether this file was imported as part of the
+    package or loaded by file path under a bare module name, the way every
+    reference harness loads its kernel file (benchmarks/run_correctness_test.py:
+    58-65: ``spec_from_file_location(clean_name, path)``)."""
+    if __package__:
+        return importlib.import_module(f"{__package__}.{name}")
+    here = os.path.dirname(os.path.abspath(__file__))
+    parent = os.path.dirname(here)
+    if parent not in sys.path:
+        sys.path.insert(0, parent)
+    mod = importlib.import_module(f"ascend_rsfa.{name}")
+    if os.path.dirname(os.path.abspath(mod.__file__)) != here:
+        raise ImportError(f"ascend_rsfa.{name} resolved to {mod.__file__}, not to the package beside "
+                          f"{__file__}; put {parent} first on sys.path")
+    return mod
+
+
+_native = _package_module("_native")
 
 __all__ = ["attention", "get_tiling", "get_num_compute_cores", "resolve_tiling", "forward",
            "split_workspace_bytes"]
@@ -74,7 +98,10 @@ def get_num_compute_cores():
     return n
 
 
-def get_tiling(Z, H, N_CTX, HEAD_DIM, causal):
+_TILING_MEMO = {}
+
+
+def get_tiling(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16):
     """Return (BLOCK_M, BLOCK_N) for the shape (reference 624-665).
 
     The reference looks the shape up in a table of Ascend tilings and raises
@@ -82,29 +109,44 @@ def get_tiling(Z, H, N_CTX, HEAD_DIM, causal):
     tiling cache answers first when one is active (``tiling.use_cache`` or
     ``RSFA_TILING_CACHE``; entries that are not a compiled tile shape are
     ignored); otherwise the library searches the compiled gfx950 tile shapes
-    with a register/LDS feasibility check and a makespan model of the
-    persistent grid, so it answers for every valid shape.
+    with an LDS feasibility check and a makespan model of the persistent grid
+    on the current device's CUs, so it answers for every valid shape.  This is
+    the tile ``attention`` runs.
     """
-    from . import tiling
-    cache = tiling.active_cache()
+    cache = _package_module("tiling").active_cache()
     if cache is not None:
-        hit = cache.lookup(Z, H, N_CTX, HEAD_DIM, causal)
-        if hit is not None:
+        entry = cache.lookup(Z, H, N_CTX, HEAD_DIM, causal, dtype)
+        if entry is not None:
             try:
-                if resolve_tiling(HEAD_DIM, causal, hit[0], hit[1]) == tuple(hit):
-                    return tuple(hit)
+                if resolve_tiling(HEAD_DIM, causal, entry[0], entry[1], dtype) == tuple(entry):
+                    return tuple(entry)
             except ValueError:
                 pass
-    bm = ctypes.c_int32()
-    bn = ctypes.c_int32()
-    st = _native.lib().rsfa_get_tiling(int(Z), int(H), int(N_CTX), int(HEAD_DIM), 1 if causal else 0,
-                                       _native.DTYPE_F16, ctypes.byref(bm), ctypes.byref(bn))
-    _raise_for(st)
-    return (bm.value, bn.value)
+    # the library's answer depends only on the shape, dtype and device: memoised
+    key = (int(Z), int(H), int(N_CTX), int(HEAD_DIM), bool(causal), dtype,
+           torch.cuda.current_device() if torch.cuda.is_available() else -1)
+    hit = _TILING_MEMO.get(key)
+    if hit is None:
+        bm = ctypes.c_int32()
+        bn = ctypes.c_int32()
+        st = _native.lib().rsfa_get_tiling(int(Z), int(H), int(N_CTX), int(HEAD_DIM), 1 if causal else 0,
+                                           _DTYPES.get(dtype, _native.DTYPE_F16), ctypes.byref(bm),
+                                           ctypes.byref(bn))
+        _raise_for(st)
+        hit = (bm.value, bn.value)
+        if len(_TILING_MEMO) > 4096:
+            _TILING_MEMO.clear()
+        _TILING_MEMO[key] = hit
+    return hit
 
 
 def resolve_tiling(HEAD_DIM, causal, BM, BN, dtype=torch.float16):
-    """The (BLOCK_M, BLOCK_N) instantiation that runs a request of (BM, BN)."""
+    """The compiled (BLOCK_M, BLOCK_N) instantiation nearest to a request.
+
+    Raises ValueError for a request the reference's rules reject.  This is the
+    tile ``forward(..., exact_tile=True)`` runs; without ``exact_tile`` a valid
+    request is a hint and the tile of ``get_tiling`` runs.
+    """
     bm = ctypes.c_int32()
     bn = ctypes.c_int32()
     st = _native.lib().rsfa_resolve_tiling(int(HEAD_DIM), 1 if causal else 0, _DTYPES.get(dtype, -1),
@@ -134,14 +176,18 @@ def _as_kernel_layout(t):
 
 
 def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=False,
-            static_schedule=False, out=None):
+            static_schedule=False, exact_tile=False, out=None):
     """Run the forward kernel; returns ``o`` or ``(o, lse)``.
 
-    ``BM = BN = 0`` lets the library pick the tiling.  ``split=True`` (causal
-    only) runs the reference's two-launch prefix/diagonal split with an fp32
-    state workspace; ``static_schedule=True`` replaces the dynamic task queue
-    by the reference's grid-stride order (results are bitwise identical).
-    ``lse`` is the natural-log logsumexp of the scaled scores, fp32 [Z, H, N].
+    ``BM``/``BN`` keep the reference's meaning and validity rules (ValueError
+    otherwise) but are a hint: the tile ``get_tiling`` picks for the shape
+    runs, as the reference's values are tuned for Ascend.  ``exact_tile=True``
+    runs the compiled tile nearest to the request instead (``resolve_tiling``);
+    ``BM = BN = 0`` is no request.  ``split=True`` (causal only) runs the
+    reference's two-launch prefix/diagonal split with an fp32 state workspace;
+    ``static_schedule=True`` replaces the dynamic task queue by the
+    reference's grid-stride order (results are bitwise identical).  ``lse`` is
+    the natural-log logsumexp of the scaled scores, fp32 [Z, H, N].
     """
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError(f"q, k, v must share one 4-D shape [Z, H, N_CTX, D]; got "
@@ -175,20 +221,24 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
         getattr(args, name)[:] = list(t.stride())
     args.sm_scale = float(sm_scale)
     args.causal = 1 if causal else 0
-    args.block_m = int(BM)
-    args.block_n = int(BN)
-    args.flags = (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
-        _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0)
     ws = None
     with torch.cuda.device(q.device):
+        # The tile is settled here and passed as an exact request, so the
+        # launch runs the same tile the split workspace is sized for, and a
+        # get_tiling answer from a measured cache is honoured.
+        if (BM or BN) and exact_tile:
+            bm, bn = resolve_tiling(D, causal, BM, BN, q.dtype)
+        else:
+            if BM or BN:
+                resolve_tiling(D, causal, BM, BN, q.dtype)  # the reference's validity rules
+            bm, bn = get_tiling(Z, H, N, D, causal, q.dtype)
+        args.block_m = bm
+        args.block_n = bn
+        args.flags = _native.FLAG_EXACT_TILE | (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
+            _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0)
         # workspace: the fp16 copy of a float8 V, then the split state
         nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0
         if split and causal:
-            bm = BM
-            if not (BM or BN):
-                bm, _ = get_tiling(Z, H, N, D, causal)
-            else:
-                bm, _ = resolve_tiling(D, causal, BM, BN, q.dtype)
             nbytes += split_workspace_bytes(Z, H, N, D, bm)
         if nbytes:
             ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)

@@ -168,10 +168,14 @@ def search_case(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16, sm_scale=0.5
     """Time and gate every candidate tiling of one shape.
 
     ``attention_fn(q, k, v, causal, sm_scale, BM, BN)`` defaults to this
-    package's ``attention``; ``candidates`` defaults to ``compiled_candidates``.
+    package's ``forward`` with ``exact_tile=True``; ``candidates`` defaults to ``compiled_candidates``.
     Returns the case record (reference layout plus ``gate``)."""
     if attention_fn is None:
-        from .flash_attention_forward import attention as attention_fn
+        from .flash_attention_forward import forward
+
+        def attention_fn(q, k, v, causal, sm_scale, bm, bn):
+            # each candidate runs its own instantiation (a plain request is a hint)
+            return forward(q, k, v, causal, sm_scale, bm, bn, exact_tile=True)
     if device is None:
         device = torch.device("cuda", torch.cuda.current_device())
     device = torch.device(device)

@@ -51,11 +51,9 @@ bool valid_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 12
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
 struct DeviceState {
-    std::once_flag once;
-    int status = RSFA_OK;
-    int num_cus = 0;
-    uint32_t* tickets = nullptr;  // kTicketSlots counters, each returns to 0 after its launch
     std::mutex mu;
+    int num_cus = 0;              // 0 until queried
+    uint32_t* tickets = nullptr;  // kTicketSlots counters, allocated by the first dynamic launch
     std::unordered_map<void*, int> stream_slot;
     std::unordered_map<const void*, int> occupancy;  // kernel -> resident workgroups per CU
 };
@@ -68,35 +66,60 @@ int current_device(int* dev) {
     return RSFA_OK;
 }
 
-DeviceState* device_state(int dev, bool need_tickets, int* status) {
-    DeviceState& ds = g_dev[dev];
-    std::call_once(ds.once, [&] {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
-            ds.status = RSFA_E_DEVICE;
-            return;
-        }
-        ds.num_cus = cus;
-        void* buf = nullptr;
-        const size_t bytes = sizeof(uint32_t) * kTicketSlots * kSlotWords;
-        if (hipMalloc(&buf, bytes) != hipSuccess || hipMemset(buf, 0, bytes) != hipSuccess ||
-            hipDeviceSynchronize() != hipSuccess) {
-            ds.status = RSFA_E_DEVICE;
-            return;
-        }
-        ds.tickets = (uint32_t*)buf;
-    });
-    (void)need_tickets;
-    *status = ds.status;
-    return ds.status == RSFA_OK ? &ds : nullptr;
+// Compute units of `dev`, queried once.  A failed query is not remembered, so
+// a later call retries it.
+int device_cus(DeviceState& ds, int dev, int* cus) {
+    std::lock_guard<std::mutex> lock(ds.mu);
+    if (ds.num_cus <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            return RSFA_E_DEVICE;
+        ds.num_cus = n;
+    }
+    *cus = ds.num_cus;
+    return RSFA_OK;
+}
+
+// CU count the tile search plans for: the current device's, or a whole
+// MI355X (256) where no device is visible, so get_tiling answers the same as
+// the launcher on a GPU and still answers without one.
+int planning_cus() {
+    int dev = 0, cus = 0;
+    if (current_device(&dev) == RSFA_OK && device_cus(g_dev[dev], dev, &cus) == RSFA_OK) return cus;
+    return 256;
+}
+
+// Whether a launch on `stream` may use a dynamic ticket counter.  The counter
+// is found by the stream handle and relies on the stream running its launches
+// one after another, which fails for launches recorded into a graph (replays
+// of graphs captured on one stream may run concurrently on other streams) and
+// for hipStreamPerThread (one handle for every thread's stream): those use the
+// static schedule, which gives bitwise the same results.
+bool dynamic_schedule_allowed(void* stream) {
+    if ((hipStream_t)stream == hipStreamPerThread) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) return false;
+    return cs == hipStreamCaptureStatusNone;
 }
 
 // Counter for launches on `stream`.  Launches on one stream run in order, and
 // each launch leaves its counter at 0 when it ends, so a stream can reuse its
-// counter; distinct streams get distinct counters.  Returns null when all
-// counters are taken (the launch then uses the static schedule).
+// counter; distinct streams get distinct counters.  The counters are allocated
+// (and zeroed) by the first call; returns null when that fails or all counters
+// are taken (the launch then uses the static schedule; a failed allocation is
+// retried by the next call).
 uint32_t* stream_ticket(DeviceState& ds, void* stream) {
     std::lock_guard<std::mutex> lock(ds.mu);
+    if (!ds.tickets) {
+        void* buf = nullptr;
+        const size_t bytes = sizeof(uint32_t) * kTicketSlots * kSlotWords;
+        if (hipMalloc(&buf, bytes) != hipSuccess) return nullptr;
+        if (hipMemset(buf, 0, bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+            (void)hipFree(buf);
+            return nullptr;
+        }
+        ds.tickets = (uint32_t*)buf;
+    }
     auto it = ds.stream_slot.find(stream);
     int slot;
     if (it != ds.stream_slot.end()) {
@@ -215,11 +238,23 @@ int choose_tiling(int64_t z, int64_t h, int64_t n, int64_t d, int causal, int dt
     return RSFA_OK;
 }
 
-int resolve(int64_t d, int causal, int dtype, int req_bm, int req_bn, const KernelEntry** out) {
+// A requested (BLOCK_M, BLOCK_N) must follow the reference's rules (powers of
+// two in [16, 512], BLOCK_M * BLOCK_N <= 65536, tiling/search_optimal_tiling.py:
+// 47-81) and, when causal, BLOCK_N <= BLOCK_M, which the reference silently
+// breaks on (NaN, benchmarks/run_correctness_test.py:24-25).
+int validate_request(int causal, int req_bm, int req_bn) {
     if (!is_pow2(req_bm) || !is_pow2(req_bn) || req_bm < 16 || req_bn < 16 || req_bm > 512 || req_bn > 512 ||
         (int64_t)req_bm * req_bn > 65536)
         return RSFA_E_TILE;
     if (causal && req_bn > req_bm) return RSFA_E_TILE;
+    return RSFA_OK;
+}
+
+// The compiled instantiation nearest to a valid request (log distance in BM
+// and BN; ties go to the larger BN).  This is what RSFA_FLAG_EXACT_TILE runs.
+int resolve_exact(int64_t d, int causal, int dtype, int req_bm, int req_bn, const KernelEntry** out) {
+    const int st = validate_request(causal, req_bm, req_bn);
+    if (st != RSFA_OK) return st;
     const KernelEntry* best = nullptr;
     double best_dist = 0.0;
     for_each_kernel([&](const KernelEntry& e) {
@@ -246,9 +281,15 @@ int check_tensor(const void* ptr, const int64_t st[4], int mult = 8) {
     if (st[3] != 1) return RSFA_E_ALIGN;
     for (int i = 0; i < 3; ++i)
         if (st[i] < 0 || (st[i] % mult) != 0) return RSFA_E_ALIGN;
-    // per-lane 32-bit byte offsets of the LDS loader cover 16 rows
-    if (st[2] >= (int64_t(1) << 25)) return RSFA_E_ALIGN;
     return RSFA_OK;
+}
+
+// The K/V loader of a tile keeps one uniform 64-bit base per tile and per-lane
+// 32-bit byte offsets that span the tile's BN rows: ((BN - 1) * row stride +
+// row width) * 2 bytes must stay below 2^32, or the offsets would wrap.
+bool loader_offsets_fit(const KernelEntry& e, int64_t row_stride) {
+    const int64_t dp = e.d < 32 ? 32 : e.d;
+    return ((int64_t)(e.bn - 1) * row_stride + dp) * 2 < (int64_t(1) << 32);
 }
 
 // Widens a float8 e5m2 V [Z, H, N, D] (strided, unit head-dim stride) into a
@@ -294,13 +335,15 @@ const char* rsfa_strerror(int status) {
     switch (status) {
         case RSFA_OK: return "success";
         case RSFA_E_NULL: return "a required pointer is NULL";
-        case RSFA_E_SHAPE: return "invalid shape: Z, H and N_CTX must be >= 1 and fit the 32-bit task index";
+        case RSFA_E_SHAPE: return "invalid shape: Z, H and N_CTX must be >= 1 and fit the 32-bit task index "
+                                  "(split mode: Z*H*N_CTX below 2^31 rows)";
         case RSFA_E_HEADDIM: return "head_dim must be one of 16, 32, 64, 128, 256";
         case RSFA_E_DTYPE: return "dtype must be float16 or bfloat16 (q, k, v, o), or float16 q, k, o with a float8_e5m2 v";
         case RSFA_E_TILE: return "invalid BLOCK_M/BLOCK_N: powers of two in [16, 512], BLOCK_M*BLOCK_N <= 65536, "
                                  "and BLOCK_N <= BLOCK_M when causal";
-        case RSFA_E_ALIGN: return "tensors need a unit last-dim stride, other strides multiple of 8 elements "
-                                  "and 16-byte aligned base pointers";
+        case RSFA_E_ALIGN: return "tensors need a unit last-dim stride, other strides multiple of 8 elements, "
+                                  "16-byte aligned base pointers, and K/V row strides that keep a key tile "
+                                  "within 4 GiB";
         case RSFA_E_DEVICE: return "HIP runtime error while preparing the device";
         case RSFA_E_LAUNCH: return "kernel launch failed";
         case RSFA_E_ABI: return "rsfa_fwd_args.struct_size does not match this library";
@@ -328,7 +371,7 @@ int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype, int32_t
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
     if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
     const KernelEntry* e = nullptr;
-    const int st = resolve(head_dim, causal, dtype, req_block_m, req_block_n, &e);
+    const int st = resolve_exact(head_dim, causal, dtype, req_block_m, req_block_n, &e);
     if (st != RSFA_OK) return st;
     *block_m = 32 * e->nw;
     *block_n = e->bn;
@@ -341,10 +384,9 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     if (z < 1 || h < 1 || n_ctx < 1) return RSFA_E_SHAPE;
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
     if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
-    // The cost model is evaluated for a 256-CU MI355X so the answer does not
-    // depend on whether a GPU is visible to the caller.
+    // the same CU count the launcher plans with (256 where no device is visible)
     const KernelEntry* e = nullptr;
-    const int st = choose_tiling(z, h, n_ctx, head_dim, causal, dtype, 256, &e);
+    const int st = choose_tiling(z, h, n_ctx, head_dim, causal, dtype, planning_cus(), &e);
     if (st != RSFA_OK) return st;
     *block_m = 32 * e->nw;
     *block_n = e->bn;
@@ -363,7 +405,12 @@ uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t
     return (uint64_t)(2 * z * h * nmb * block_m) * sizeof(float);
 }
 
-int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
+// Shared body of the launch entry points.  `ws` / `ws_bytes` is the
+// workspace the launch may use (float8 V copy, split state) and `tickets`
+// where its dynamic queue counters live: null lets it take this stream's
+// counter from the library's allocation.
+static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t ws_bytes, uint32_t* tickets,
+                      bool tickets_given) {
     if (!a) return RSFA_E_NULL;
     if (a->struct_size != sizeof(rsfa_fwd_args)) return RSFA_E_ABI;
     if (!a->q || !a->k || !a->v || !a->o) return RSFA_E_NULL;
@@ -380,17 +427,36 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     if (((uintptr_t)a->lse & 3) != 0) return RSFA_E_ALIGN;
     const bool causal = a->causal != 0;
     const bool split = causal && (a->flags & RSFA_FLAG_CAUSAL_SPLIT);
+    if ((a->block_m != 0 || a->block_n != 0) &&
+        (st = validate_request(causal ? 1 : 0, a->block_m, a->block_n)) != RSFA_OK)
+        return st;
+    // Limits of the kernels' index arithmetic, checked for every tile the
+    // launch could pick (before any device work): the K/V loader's per-lane
+    // 32-bit offsets, and the split state's 32-bit rows (task * BLOCK_M + row
+    // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
+    const int64_t v_rows = v8 ? a->head_dim : a->v_stride[2];  // a float8 V is read from its fp16 copy
+    for_each_kernel([&](const KernelEntry& e) {
+        if (st == RSFA_OK && e.dtype == a->dtype && e.d == a->head_dim &&
+            (!loader_offsets_fit(e, a->k_stride[2]) || !loader_offsets_fit(e, v_rows)))
+            st = RSFA_E_ALIGN;
+    });
+    if (st != RSFA_OK) return st;
+    if (split && a->z * a->h * ((a->n_ctx + 255) / 256 * 256) >= (int64_t(1) << 31)) return RSFA_E_SHAPE;
 
     int dev = 0;
     if ((st = current_device(&dev)) != RSFA_OK) return st;
-    DeviceState* ds = device_state(dev, true, &st);
-    if (!ds) return st;
+    DeviceState& ds = g_dev[dev];
+    int num_cus = 0;
+    if ((st = device_cus(ds, dev, &num_cus)) != RSFA_OK) return st;
 
+    // A valid (BLOCK_M, BLOCK_N) request is a hint, as it is a tuning knob of
+    // the reference: the launch runs the tile the search picks for the shape,
+    // unless RSFA_FLAG_EXACT_TILE asks for the nearest compiled one.
     const KernelEntry* e = nullptr;
-    if (a->block_m == 0 && a->block_n == 0)
-        st = choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, ds->num_cus, &e);
+    if ((a->flags & RSFA_FLAG_EXACT_TILE) && (a->block_m != 0 || a->block_n != 0))
+        st = resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, &e);
     else
-        st = resolve(a->head_dim, causal, a->dtype, a->block_m, a->block_n, &e);
+        st = choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, num_cus, &e);
     if (st != RSFA_OK) return st;
     const int bm = 32 * e->nw;
 
@@ -424,12 +490,12 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
     if (v8 || split) {
         const uint64_t need =
             v8_bytes + (split ? rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm) : 0);
-        if (!a->workspace || a->workspace_bytes < need) return RSFA_E_WORKSPACE;
-        if (((uintptr_t)a->workspace & (v8 ? 15 : 3)) != 0) return RSFA_E_ALIGN;
-        if (split) p.state = (float*)((char*)a->workspace + v8_bytes);
+        if (!ws || ws_bytes < need) return RSFA_E_WORKSPACE;
+        if (((uintptr_t)ws & (v8 ? 15 : 3)) != 0) return RSFA_E_ALIGN;
+        if (split) p.state = (float*)((char*)ws + v8_bytes);
     }
     if (v8) {
-        uint32_t* wide = (uint32_t*)a->workspace;
+        uint32_t* wide = (uint32_t*)ws;
         const int lcpr = a->head_dim == 16 ? 0 : a->head_dim == 32 ? 1 : a->head_dim == 64 ? 2
                          : a->head_dim == 128 ? 3 : 4;  // log2 of the 16-byte chunks per row
         const int64_t per_head = a->n_ctx << lcpr;
@@ -444,24 +510,30 @@ int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
         p.v_sz = a->h * p.v_sh;
     }
 
-    const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE);
+    const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE) && (tickets_given || dynamic_schedule_allowed(stream));
     const int modes[2] = {split ? MODE_PREFIX : MODE_FUSED, MODE_DIAG};
     const int launches = split ? 2 : 1;
     for (int li = 0; li < launches; ++li) {
         const KernelEntry* k = find_kernel(a->dtype, (int)a->head_dim, e->bn, e->nw, causal ? 1 : 0, modes[li]);
         if (!k) return RSFA_E_TILE;
-        const int wgs = resident_wgs(*ds, *k);
-        int64_t grid = (int64_t)ds->num_cus * wgs;
+        const int wgs = resident_wgs(ds, *k);
+        int64_t grid = (int64_t)num_cus * wgs;
         grid = std::min<int64_t>(grid, p.num_tasks);
         grid = std::max<int64_t>(grid, 1);
         p.nq = queue_count(p.num_heads, grid);
-        p.ticket = dynamic ? stream_ticket(*ds, stream) : nullptr;
+        p.ticket = !dynamic ? nullptr : tickets_given ? tickets : stream_ticket(ds, stream);
         void* args[] = {&p};
         if (hipLaunchKernel(k->fn, dim3((unsigned)grid), dim3((unsigned)(k->nw * 64)), args, 0,
                             (hipStream_t)stream) != hipSuccess)
             return RSFA_E_LAUNCH;
     }
     return RSFA_OK;
+}
+
+int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {
+    if (!a) return RSFA_E_NULL;
+    if (a->struct_size != sizeof(rsfa_fwd_args)) return RSFA_E_ABI;
+    return fwd_launch(a, stream, a->workspace, a->workspace_bytes, nullptr, false);
 }
 
 }  // extern "C"

@@ -3,11 +3,18 @@
 Prints ONE JSON line.  A step is one ``attention(q, k, v, causal, sm_scale,
 BM, BN)`` call (the reference's public entry point) over the workload's
 seeded synthetic Q/K/V, already resident in HBM.  ``value`` is the algorithmic
-throughput 4*B*H*S^2*D (x0.5 causal) / time in TFLOP/s of the BASELINE workload
-configs[1] (non-causal B=32 H=8 S=2048 D=128), timed as K back-to-back calls
-between two HIP events on the stream the kernel is launched on.  The other
-BASELINE configs and the north-star target shape are timed the same way and
-reported under ``"configs"``.
+throughput 4*B*H*S^2*D (x0.5 causal) / time in TFLOP/s of the north-star
+non-causal shape B=128 H=8 S=2048 D=128 (the reference's benchmark case 09,
+benchmarks/benchmark_results.txt:21), timed as K back-to-back calls between
+two HIP events on the stream the kernel is launched on.  The causal target
+(C3: B=128 H=8 S=2048 D=128, the reference's case 03)
+gets its own roofline object beside it; the other BASELINE configs are timed
+the same way and reported under ``"configs"``.
+
+Inputs follow the BASELINE recipe: Q, K, V ~ N(0, 1) drawn in fp32 by
+``torch.Generator('cpu')`` from a per-config seed (q, k, v order), cast to
+fp16, copied to the GPU; their SHA-256 is compared with the committed
+fingerprints (tests/golden/input_fingerprints.json) where one exists.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
                     [--calibrate-copy-mib M]
@@ -18,9 +25,11 @@ the counter reading of a kernel with known traffic, which scales the readings
 of the attention kernel to bytes.
 """
 import argparse
+import hashlib
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -34,9 +43,11 @@ PEAK_HBM_GBS = 8000.0
 
 # name, B, H, S, D, causal, sm_scale, seed[, V dtype]
 CONFIGS = [
-    ("C2", 32, 8, 2048, 128, False, 1 / math.sqrt(128), 1236),   # the `value`
-    ("C3", 128, 8, 2048, 128, True, 0.5, 1237),
+    # the headline (`value`): north-star non-causal shape, reference case 09
     ("target-noncausal", 128, 8, 2048, 128, False, 1 / math.sqrt(128), 1240),
+    # the causal target, reference case 03
+    ("C3", 128, 8, 2048, 128, True, 0.5, 1237),
+    ("C2", 32, 8, 2048, 128, False, 1 / math.sqrt(128), 1236),
     ("C4-noncausal", 64, 8, 1024, 256, False, 1 / 16, 1238),
     ("C4-causal", 64, 8, 1024, 256, True, 1 / 16, 1238),
     ("C5", 4, 16, 8192, 64, True, 1 / 8, 1239),
@@ -44,8 +55,14 @@ CONFIGS = [
     # the reference's fp8_v branch (flash_attention_forward.py:208-211): fp16 Q, K, O, float8 e5m2 V
     ("C2-v8e5m2", 32, 8, 2048, 128, False, 1 / math.sqrt(128), 1236, "e5m2"),
 ]
-# HBM bytes per launch of the C2 kernel, from two rocprofv3 --pmc passes
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "fa_fwd_c2_traffic.txt")
+HEADLINE = "target-noncausal"
+CAUSAL_TARGET = "C3"
+FINGERPRINTS = os.path.join(ROOT, "tests", "golden", "input_fingerprints.json")
+# fingerprint keys of configs that share a draw
+FINGERPRINT_KEY = {"C4-noncausal": "C4", "C4-causal": "C4"}
+# seconds of back-to-back launches before the first timed config: the clocks
+# start high and settle under sustained MFMA load
+DEVICE_WARMUP_S = 2.0
 
 
 def flops(B, H, S, D, causal):
@@ -58,17 +75,61 @@ def algo_bytes(B, H, S, D, causal, v_bytes=2):
     return (2.0 * 3 + v_bytes) * B * H * S * D + (0.0 if causal else 4.0 * B * H * S)
 
 
-def time_config(F, torch, cfg, steps, warmup):
+def profile_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary of this workload, or None when there is none."""
+    path = os.path.join(ROOT, "profiles", f"fa_fwd_{name.lower().replace('-', '_')}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def make_inputs(torch, cfg):
+    """Seeded fp16 Q, K, V (V float8 e5m2 for the fp8-V config) on the CPU."""
     name, B, H, S, D, causal, scale, seed = cfg[:8]
-    v8 = len(cfg) > 8 and cfg[8] == "e5m2"
-    g = torch.Generator(device="cuda")
+    g = torch.Generator(device="cpu")
     g.manual_seed(seed)
     shape = (B, H, S, D)
-    q = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).half()
-    k = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).half()
-    v = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32)
-    v = v.to(torch.float8_e5m2) if v8 else v.half()
+    q = torch.randn(shape, generator=g, dtype=torch.float32).half()
+    k = torch.randn(shape, generator=g, dtype=torch.float32).half()
+    v = torch.randn(shape, generator=g, dtype=torch.float32)
+    v = v.to(torch.float8_e5m2) if (len(cfg) > 8 and cfg[8] == "e5m2") else v.half()
+    return q, k, v
+
+
+def fingerprint_check(torch, name, tensors):
+    key = FINGERPRINT_KEY.get(name, name)
+    try:
+        with open(FINGERPRINTS) as f:
+            want = json.load(f)["configs"].get(key, {}).get("sha256")
+    except OSError:
+        want = None
+    if want is None or tensors[2].dtype != torch.float16:
+        return None
+    h = hashlib.sha256()
+    for t in tensors:
+        h.update(memoryview(t.contiguous().view(torch.uint8).numpy()))
+    return h.hexdigest() == want
+
+
+def time_config(F, torch, cfg, steps, warmup, device_warmup_s=0.0, keep_cpu=False):
+    name, B, H, S, D, causal, scale, seed = cfg[:8]
+    v8 = len(cfg) > 8 and cfg[8] == "e5m2"
+    q_c, k_c, v_c = make_inputs(torch, cfg)
+    fp_ok = fingerprint_check(torch, name, (q_c, k_c, v_c))
+    q, k, v = q_c.cuda(), k_c.cuda(), v_c.cuda()
     BM, BN = F.get_tiling(B, H, S, D, causal)
+    if device_warmup_s > 0:
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        while time.perf_counter() - t < device_warmup_s:
+            for _ in range(20):
+                F.attention(q, k, v, causal, scale, BM, BN)
+            torch.cuda.synchronize()
     for _ in range(warmup):
         F.attention(q, k, v, causal, scale, BM, BN)
     # attention() enqueues its kernel on the current stream: the events go there
@@ -85,13 +146,23 @@ def time_config(F, torch, cfg, steps, warmup):
     fl = flops(B, H, S, D, causal)
     del q, k, v
     torch.cuda.empty_cache()
-    return {
-        "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "tiling": [BM, BN],
+    res = {
+        "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "seed": seed, "tiling": [BM, BN],
         "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
         "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
         "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal, 1 if v8 else 2) / (ms * 1e-3) / 1e9, 1),
+        "inputs_match_fingerprint": fp_ok,
         **({"v_dtype": "float8_e5m2"} if v8 else {}),
     }
+    return res, ((q_c, k_c, v_c) if keep_cpu else None)
+
+
+def roofline(cfg, res):
+    """MFMA roofline of one config's kernel: algorithmic FLOPs per launch over
+    the average launch duration of the timed region."""
+    achieved = flops(*cfg[1:6]) / (res["ms_per_call"] * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": profile_traffic(cfg[0])}
 
 
 def calibrate_copy(torch, mib):
@@ -106,37 +177,61 @@ def calibrate_copy(torch, mib):
     print(f"[bench] calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(torch, cfg, budget_s=10.0):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def host_threads():
+    """Threads for the CPU baseline: the host's cores as os.cpu_count() reports
+    them, capped by this process's CPU affinity and an OMP_NUM_THREADS limit
+    (the GPU box's share of its host)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_baseline(torch, cfg, inputs, budget_s=12.0):
     """The reference's attention math (the oracle's fp32 closed form) on the host cores.
 
-    Bounded sample: whole heads of the workload, repeated until about
-    ``budget_s`` seconds of CPU time have run.
+    Bounded sample: the first heads of the workload's own inputs, as many as
+    about ``budget_s`` seconds of CPU time allow.
     """
     from oracle import attention as oracle
 
-    name, B, H, S, D, causal, scale, seed = cfg
-    threads = torch.get_num_threads()
-    q, k, v = oracle.make_inputs(1, 1, S, D, seed)
-    oracle.reference_attention(q, k, v, causal, scale)  # warmup
+    name, B, H, S, D, causal, scale, seed = cfg[:8]
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    q, k, v = (t.reshape(B * H, S, D) for t in inputs)
+    one = lambda n: oracle.reference_attention(q[:n][None], k[:n][None], v[:n][None], causal, scale)  # noqa: E731
+    one(1)  # warmup
     t = time.perf_counter()
-    oracle.reference_attention(q, k, v, causal, scale)
-    one = max(time.perf_counter() - t, 1e-4)
-    heads = max(1, min(B * H, int(budget_s / one)))
-    q, k, v = oracle.make_inputs(1, heads, S, D, seed)
-    reps = 0
+    one(2)
+    per_head = max((time.perf_counter() - t) / 2, 1e-4)
+    heads = max(1, min(B * H, int(budget_s / per_head)))
     t = time.perf_counter()
-    while True:
-        oracle.reference_attention(q, k, v, causal, scale)
-        reps += 1
-        el = time.perf_counter() - t
-        if el >= budget_s * 0.5 or reps >= 20:
-            break
-    fl = flops(1, heads, S, D, causal) * reps
+    one(heads)
+    el = time.perf_counter() - t
+    fl = flops(1, heads, S, D, causal)
     return {
         "value": round(fl / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": f"{reps} x {heads} of {B * H} heads of {name} (S={S}, D={D}, causal={causal}): the fp32 closed "
-                  f"form softmax(QK^T*scale)V in PyTorch on {threads} host threads, {el:.1f} s; "
-                  f"full S^2 computed even when causal; FLOPs counted as on the GPU",
+        "sample": f"{heads} of {B * H} heads of {name} (S={S}, D={D}, causal={causal}, the bench's own inputs): "
+                  f"the fp32 closed form softmax(QK^T*scale)V in PyTorch, {el:.1f} s; full S^2 computed even "
+                  f"when causal; FLOPs counted as on the GPU",
+        "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(), "cpu_model": cpu_model(),
+        "ms_per_call_extrapolated": round(el / heads * B * H * 1e3, 1),
     }
 
 
@@ -167,22 +262,21 @@ def main():
     torch.cuda.set_device(0)
     configs = [c for c in CONFIGS if args.only in (None, c[0])]
     results = {}
-    for cfg in configs:
-        results[cfg[0]] = time_config(F, torch, cfg, args.steps, args.warmup)
+    head_inputs = None
+    for i, cfg in enumerate(configs):
+        keep = i == 0 and not args.no_cpu
+        results[cfg[0]], kept = time_config(F, torch, cfg, args.steps, args.warmup,
+                                            device_warmup_s=DEVICE_WARMUP_S if i == 0 else 0.0, keep_cpu=keep)
+        if keep:
+            head_inputs = kept
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
     if args.calibrate_copy_mib:
         calibrate_copy(torch, args.calibrate_copy_mib)
-    main_name = configs[0][0]
-    r = results[main_name]
     cfg = configs[0]
-    # average duration of one launch over the timed region (back-to-back launches)
-    achieved = flops(*cfg[1:6]) / (r["ms_per_call"] * 1e-3) / 1e12
-    traffic = None
-    if main_name == "C2" and os.path.exists(PROFILE_TRAFFIC):
-        with open(PROFILE_TRAFFIC) as f:
-            for line in f:
-                if line.startswith("hbm_bytes_per_launch:"):
-                    traffic = int(float(line.split(":", 1)[1]))
+    r = results[cfg[0]]
+    by_name = {c[0]: c for c in configs}
+    for name, res in results.items():
+        res["roofline_frac"] = roofline(by_name[name], res)["frac"]
     line = {
         "metric": METRIC,
         "value": r["tflops"],
@@ -195,17 +289,23 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic: seeded Q,K,V ~ N(0,1) fp16, resident in HBM",
-        "config": {"workload": f"{main_name}: B={cfg[1]} H={cfg[2]} S={cfg[3]} D={cfg[4]} "
+        "data": "synthetic: Q,K,V ~ N(0,1) drawn in fp32 by torch.Generator('cpu') from a per-config seed, "
+                "cast to fp16, resident in HBM",
+        "config": {"workload": f"{cfg[0]}: B={cfg[1]} H={cfg[2]} S={cfg[3]} D={cfg[4]} "
                                f"{'causal' if cfg[5] else 'non-causal'} sm_scale={cfg[6]:.6g}",
                    "layout": "[B,H,S,D]", "tiling": r["tiling"], "parallelism": "single GPU"},
         "pct_peak": r["pct_peak"],
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic},
+        "roofline": roofline(cfg, r),
+        "device_warmup_s": DEVICE_WARMUP_S,
         "configs": results,
     }
+    if CAUSAL_TARGET in results and cfg[0] != CAUSAL_TARGET:
+        rc = results[CAUSAL_TARGET]
+        line["causal_target"] = {"workload": f"{CAUSAL_TARGET}: B=128 H=8 S=2048 D=128 causal sm_scale=0.5",
+                                 "ms_per_call": rc["ms_per_call"], "tflops": rc["tflops"],
+                                 "roofline": roofline(by_name[CAUSAL_TARGET], rc)}
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(torch, cfg)
+        line["cpu_baseline"] = cpu_baseline(torch, cfg, head_inputs)
     print(json.dumps(line), flush=True)
 
 

@@ -26,8 +26,11 @@
  *   - All tensor pointers are device pointers owned by the caller; the library
  *     never frees them.  Strides are in elements.  The last (head-dim) stride
  *     of q/k/v/o must be 1, every other stride a multiple of 8 elements (16
- *     for a float8 V) and every base pointer 16-byte aligned (RSFA_E_ALIGN
- *     otherwise).
+ *     for a float8 V) and every base pointer 16-byte aligned.  The K and V
+ *     row strides must also keep one key tile inside 4 GiB:
+ *     ((BLOCK_N - 1) * row_stride + max(D, 32)) * 2 < 2^32 bytes for the
+ *     tile that runs (BLOCK_N <= 128: row strides below ~16.9 M elements
+ *     always pass).  RSFA_E_ALIGN otherwise.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t, NULL = the
  *     null stream).  The call returns after the launch, not after completion.
  *   - Return codes: 0 on success, a negative rsfa_status otherwise.  Invalid
@@ -42,7 +45,7 @@
 extern "C" {
 #endif
 
-#define RSFA_ABI_VERSION 2
+#define RSFA_ABI_VERSION 3
 
 typedef enum rsfa_status {
     RSFA_OK          = 0,
@@ -78,6 +81,10 @@ typedef enum rsfa_dtype {
                                           prefix then masked diagonal, with the
                                           (m, l, acc) state handed over through
                                           `workspace` (reference 493-541)       */
+#define RSFA_FLAG_EXACT_TILE      0x4u /* run the compiled tile nearest to
+                                          (block_m, block_n) instead of the
+                                          tile rsfa_get_tiling picks (used to
+                                          time or test one instantiation)       */
 
 typedef struct rsfa_fwd_args {
     uint32_t    struct_size;  /* = sizeof(rsfa_fwd_args)                        */
@@ -100,8 +107,13 @@ typedef struct rsfa_fwd_args {
     int64_t     o_stride[4];
     float       sm_scale;     /* multiplies q.k before the softmax              */
     int32_t     causal;       /* 0/1: key n visible to query m iff n <= m       */
-    int32_t     block_m;      /* requested BLOCK_M, 0 = choose (rsfa_get_tiling)*/
-    int32_t     block_n;      /* requested BLOCK_N, 0 = choose                  */
+    int32_t     block_m;      /* requested BLOCK_M; 0 (with block_n 0) = no
+                                 request.  A request is checked against the
+                                 reference's rules (RSFA_E_TILE otherwise) and
+                                 is a hint, like the reference's tuning knob:
+                                 the launch runs the tile rsfa_get_tiling picks
+                                 for the shape, unless RSFA_FLAG_EXACT_TILE    */
+    int32_t     block_n;      /* requested BLOCK_N (see block_m)                */
     uint32_t    flags;        /* RSFA_FLAG_*                                    */
 } rsfa_fwd_args;
 
@@ -122,14 +134,16 @@ uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                  int64_t head_dim);
 
 /* Tile search for gfx950 (replaces the lookup table get_tiling, 624-665):
- * writes the (BLOCK_M, BLOCK_N) this library would pick for the shape.
- * Never fails for a valid shape. */
+ * writes the (BLOCK_M, BLOCK_N) rsfa_attention_fwd runs for the shape on the
+ * current device (planned for its CU count; for a 256-CU MI355X where no
+ * device is visible).  Never fails for a valid shape. */
 int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim,
                     int32_t causal, int32_t dtype, int32_t *block_m,
                     int32_t *block_n);
 
 /* Maps a caller-requested (BLOCK_M, BLOCK_N) to the compiled instantiation
- * that runs it.  Requests follow the reference's rules (powers of two,
+ * that runs it under RSFA_FLAG_EXACT_TILE (the nearest compiled tile).
+ * Requests follow the reference's rules (powers of two,
  * 16 <= BLOCK <= 512, BLOCK_M*BLOCK_N <= 65536, causal needs
  * BLOCK_N <= BLOCK_M, which the reference silently breaks on, see
  * benchmarks/run_correctness_test.py:24-25).  Returns RSFA_E_TILE otherwise. */

@@ -1,6 +1,6 @@
 """Write tests/golden/input_fingerprints.json: SHA-256 of the seeded fp16 Q, K, V
 of the five BASELINE configurations (oracle.attention.make_inputs, seeds 1234 +
-config index), so a machine that regenerates them can tell whether its torch
+config index) and of the north-star non-causal shape (seed 1240), so a machine that regenerates them can tell whether its torch
 draws the same inputs.  A mismatch is reported by the tests, it does not void
 parity (the oracle is recomputed from the same inputs in the same run).
 
@@ -22,6 +22,8 @@ CONFIGS = [
     ("C3", 128, 8, 2048, 128, 1237),
     ("C4", 64, 8, 1024, 256, 1238),
     ("C5", 4, 16, 8192, 64, 1239),
+    # the north-star non-causal shape (B=128 H=8 S=2048 D=128), timed by bench.py
+    ("target-noncausal", 128, 8, 2048, 128, 1240),
 ]
 
 

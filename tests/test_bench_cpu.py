@@ -28,3 +28,38 @@ def test_work_and_byte_counts_follow_the_stated_formulas():
     assert bench.algo_bytes(128, 8, 2048, 128, True) == 8 * 128 * 8 * 2048 * 128
     # a float8 V is read as one byte per element
     assert bench.algo_bytes(32, 8, 2048, 128, False, v_bytes=1) == 7 * 32 * 8 * 2048 * 128 + 4 * 32 * 8 * 2048
+
+
+def test_inputs_follow_the_fingerprinted_recipe():
+    import torch
+
+    c1 = next(c for c in bench.CONFIGS if c[0] == "C1")
+    q, k, v = bench.make_inputs(torch, c1)
+    assert q.dtype == k.dtype == v.dtype == torch.float16 and q.device.type == "cpu"
+    assert bench.fingerprint_check(torch, "C1", (q, k, v)) is True
+    # another draw does not match
+    assert bench.fingerprint_check(torch, "C1", (k, q, v)) is False
+
+
+def test_headline_is_the_north_star_shape_and_c3_is_beside_it():
+    name, B, H, S, D, causal, scale, seed = bench.CONFIGS[0][:8]
+    assert (name, B, H, S, D, causal) == ("target-noncausal", 128, 8, 2048, 128, False) == (bench.HEADLINE,) + (
+        128, 8, 2048, 128, False)
+    assert abs(scale - 128 ** -0.5) < 1e-12
+    c3 = next(c for c in bench.CONFIGS if c[0] == bench.CAUSAL_TARGET)
+    assert c3[1:7] == (128, 8, 2048, 128, True, 0.5)
+
+
+def test_cpu_baseline_reports_cores_and_model():
+    import torch
+
+    cfg = ("tiny", 1, 2, 128, 64, True, 0.5, 7)
+    inputs = bench.make_inputs(torch, cfg)
+    before = torch.get_num_threads()
+    try:
+        cb = bench.cpu_baseline(torch, cfg, inputs, budget_s=0.2)
+    finally:
+        torch.set_num_threads(before)
+    assert cb["kind"] == "port" and cb["unit"] == "TFLOP/s" and cb["value"] > 0
+    assert cb["cores"] == bench.host_threads() >= 1 and cb["os_cpu_count"] == os.cpu_count()
+    assert isinstance(cb["cpu_model"], str) and cb["cpu_model"]

@@ -176,6 +176,16 @@ def _valid_args(**over):
     (dict(dtype=3), _native.E_DTYPE),
     # a float8 V needs 16-byte rows: outer strides a multiple of 16 elements
     (dict(dtype=_native.DTYPE_F16_V8E5M2, v_stride=[3 * 128 * 72, 128 * 72, 72, 1]), _native.E_ALIGN),
+    # tile requests follow the reference's rules even though they are hints
+    (dict(block_m=48, block_n=64), _native.E_TILE),
+    (dict(block_m=64, block_n=256, causal=1), _native.E_TILE),
+    # K/V row strides whose 128-row key tile (D=64) spans 4 GiB: the loader's
+    # 32-bit per-lane offsets would wrap, so they are refused before launch
+    (dict(k_stride=[0, 0, 16909320, 1]), _native.E_ALIGN),
+    (dict(v_stride=[0, 0, 16909320, 1]), _native.E_ALIGN),
+    (dict(head_dim=256, k_stride=[0, 0, 69273664, 1]), _native.E_ALIGN),
+    # the split state's rows are 32-bit: Z*H*N_CTX (rounded up to 256) < 2^31
+    (dict(z=1024, h=1024, n_ctx=2048, causal=1, flags=_native.FLAG_CAUSAL_SPLIT), _native.E_SHAPE),
 ])
 def test_attention_fwd_rejects_invalid_arguments(over, code):
     lib = _native.lib()
@@ -188,3 +198,18 @@ def test_attention_fwd_without_gpu_reports_device_error():
         pytest.skip("a GPU is visible; this check needs a machine without one")
     lib = _native.lib()
     assert lib.rsfa_attention_fwd(ctypes.byref(_valid_args()), None) == _native.E_DEVICE
+
+
+@pytest.mark.parametrize("over", [
+    dict(k_stride=[0, 0, 16909312, 1]),            # the largest 8-multiple row stride whose 128-row tile fits
+    dict(head_dim=256, k_stride=[0, 0, 69273656, 1]),
+    dict(z=1024, h=1024, n_ctx=2048, causal=1),     # fused causal has no split-state limit
+    dict(block_m=128, block_n=64, causal=1),        # a valid request (a hint)
+])
+def test_attention_fwd_limits_admit_the_boundary(over):
+    """Arguments just inside the index limits pass every check made before
+    device work: without a GPU the call gets as far as the device query."""
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible; this check needs a machine without one")
+    lib = _native.lib()
+    assert lib.rsfa_attention_fwd(ctypes.byref(_valid_args(**over)), None) == _native.E_DEVICE

@@ -225,7 +225,7 @@ def _fingerprints():
 
 def test_input_fingerprints_cover_the_baseline_configs_and_match_c1():
     fp = _fingerprints()
-    assert sorted(fp) == ["C1", "C2", "C3", "C4", "C5"]
+    assert sorted(fp) == ["C1", "C2", "C3", "C4", "C5", "target-noncausal"]
     c1 = fp["C1"]
     q, k, v = A.make_inputs(*c1["shape"], c1["seed"])
     assert A.fingerprint(q, k, v) == c1["sha256"]

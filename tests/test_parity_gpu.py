@@ -131,12 +131,16 @@ def test_reference_test_op_cases(Z, H, N_CTX, HEAD_DIM, causal, dtype, BM, BN):
     qd.requires_grad_()
     kd.requires_grad_()
     vd.requires_grad_()
+    # the request as a hint (the drop-in path: get_tiling's tile runs), then
+    # the compiled tile nearest to it
     out = F.attention(qd, kd, vd, causal, 0.5, BM, BN).to(dtype)
+    exact = F.forward(qd.detach(), kd.detach(), vd.detach(), causal, 0.5, BM, BN, exact_tile=True)
     torch.cuda.synchronize()
     heads = _sample_heads(Z, H, 32, 7)
     ref = A.reference_attention(q, k, v, causal, 0.5, heads=heads)
-    got = torch.stack([out.detach()[z, h] for z, h in heads])
-    _assert_close(got, ref, f"test_op{(Z, H, N_CTX, HEAD_DIM, causal, dtype, BM, BN)}")
+    for label, o in (("hint", out), ("exact", exact)):
+        got = torch.stack([o.detach()[z, h] for z, h in heads])
+        _assert_close(got, ref, f"test_op{(Z, H, N_CTX, HEAD_DIM, causal, dtype, BM, BN)} {label}")
 
 
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
@@ -232,8 +236,8 @@ def test_dynamic_and_static_schedules_bitwise_equal(causal):
 def test_causal_two_launch_split_matches_fused(BM, BN):
     q, k, v = A.make_inputs(2, 4, 1024, 64, seed=16)
     qd, kd, vd = _to_gpu(q, k, v)
-    fused = F.forward(qd, kd, vd, True, 0.125, BM, BN)
-    split = F.forward(qd, kd, vd, True, 0.125, BM, BN, split=True)
+    fused = F.forward(qd, kd, vd, True, 0.125, BM, BN, exact_tile=True)
+    split = F.forward(qd, kd, vd, True, 0.125, BM, BN, split=True, exact_tile=True)
     ref = A.reference_attention(q, k, v, True, 0.125)
     _assert_close(fused, ref, "fused")
     _assert_close(split, ref, "split")
@@ -269,8 +273,8 @@ def test_causal_diagonal_in_pingpong_matches_masked_body(dtype, N):
     q, k, v = A.make_inputs(Z, H, N, D, seed=N + 31, dtype=dtype)
     qd, kd, vd = _to_gpu(q, k, v)
     print(f"diag ping-pong: N={N} {dtype}", flush=True)
-    fused = F.forward(qd, kd, vd, True, 0.3, 256, 64)
-    split = F.forward(qd, kd, vd, True, 0.3, 256, 64, split=True)
+    fused = F.forward(qd, kd, vd, True, 0.3, 256, 64, exact_tile=True)
+    split = F.forward(qd, kd, vd, True, 0.3, 256, 64, split=True, exact_tile=True)
     ref = A.reference_attention(q, k, v, True, 0.3)
     _assert_close(fused, ref, f"fused N={N}")
     _assert_close(split, ref, f"split N={N}")
@@ -294,7 +298,7 @@ def test_d256_epilogue_column_rounds(causal, N):
     print(f"D=256 column rounds: N={N} causal={causal}", flush=True)
     for bm, bn in ((256, 32), (128, 32)):
         out = torch.full_like(qd, float("nan"))
-        F.forward(qd, kd, vd, causal, 1 / 16, bm, bn, out=out)
+        F.forward(qd, kd, vd, causal, 1 / 16, bm, bn, out=out, exact_tile=True)
         _assert_close(out, A.reference_attention(q, k, v, causal, 1 / 16), f"D=256 ({bm},{bn}) N={N}")
 
 

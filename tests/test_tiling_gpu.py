@@ -28,7 +28,7 @@ def test_a_corrupted_tiling_is_rejected_and_cannot_win():
     bad = sorted(cands)[0]
 
     def fn(q, k, v, causal, sm_scale, bm, bn):
-        o = faf.attention(q, k, v, causal, sm_scale, bm, bn)
+        o = faf.forward(q, k, v, causal, sm_scale, bm, bn, exact_tile=True)
         if (bm, bn) == bad:
             o = o.clone()
             o[0, 0, 7, 3] = float("nan")
