@@ -39,6 +39,11 @@ HIPCC_FLAGS = [
     "-I" + os.path.join(REPO_ROOT, "include"),
 ]
 
+# Per-file flags.  kern_wide.hip: MFMAs in the VGPR form (accumulators in
+# VGPRs) for the one-wave-per-SIMD kernel; the compiler then places values
+# only MFMAs read (the Q^T operands) in AGPRs.
+FILE_FLAGS = {"kern_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
 
 def hipcc():
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -67,7 +72,7 @@ def build(jobs=None, verbose=False):
 
     def compile_one(src):
         obj = os.path.join(obj_dir, src[:-4] + ".o")
-        rc, out = _run([cc] + HIPCC_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj])
+        rc, out = _run([cc] + HIPCC_FLAGS + FILE_FLAGS.get(src, []) + ["-c", os.path.join(CSRC, src), "-o", obj])
         return src, obj, rc, out
 
     jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))

@@ -30,7 +30,8 @@ constexpr int kTicketStrideWords = 16;  // one 64-byte line per counter
 constexpr int kSlotWords = kQueues * kTicketStrideWords;
 constexpr int kLdsPerCu = 160 * 1024;   // gfx950
 
-KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256()};
+KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256(),
+                          kernels_wide()};
 
 template <class F>
 void for_each_kernel(F&& f) {
@@ -38,14 +39,18 @@ void for_each_kernel(F&& f) {
         for (int i = 0; i < l.count; ++i) f(l.entries[i]);
 }
 
-const KernelEntry* find_kernel(int dtype, int d, int bn, int nw, int causal, int mode) {
+const KernelEntry* find_kernel(int dtype, int d, int bn, int bm, int causal, int mode) {
     const KernelEntry* hit = nullptr;
     for_each_kernel([&](const KernelEntry& e) {
-        if (e.dtype == dtype && e.d == d && e.bn == bn && e.nw == nw && e.causal == causal && e.mode == mode)
+        if (e.dtype == dtype && e.d == d && e.bn == bn && e.bm == bm && e.causal == causal && e.mode == mode)
             hit = &e;
     });
     return hit;
 }
+
+// Whether an instantiation can run a sequence of n_ctx keys: the
+// one-wave-per-SIMD kernel needs whole key tiles.
+bool runs_shape(const KernelEntry& e, int64_t n_ctx) { return !e.wide || n_ctx % e.bn == 0; }
 
 bool valid_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -176,6 +181,14 @@ struct TileCost {
 // other wave's MFMAs.
 double wave_tile_cycles(const KernelEntry& e) {
     const int dp = e.d < 32 ? 32 : e.d;
+    if (e.wide) {
+        // 32 * wide rows per wave: both contractions on MFMA with the softmax
+        // interleaved into them, one barrier per pair of tiles.  Measured on
+        // MI355X (B=128 H=8 S=2048 D=128): 1024 TFLOP/s for 32 rows per wave,
+        // 1002 for 64, against 1103 for the ping-pong (256, 64) tile.
+        const double mfma = 2.0 * 2.0 * 32.0 * e.wide * e.bn * dp / 1024.0;
+        return mfma * (e.wide == 1 ? 1.53 : 1.57) + 60.0;
+    }
     const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0;
     const double valu = (9.5 * e.bn / 2.0 + 300.0 * e.bn / 64.0) * (e.pp ? 0.75 : 1.0);
     const double sync = e.nw >= 8 ? 100.0 : 300.0;
@@ -187,12 +200,12 @@ TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int nu
     const int dp = e.d < 32 ? 32 : e.d;
     // Each instantiation was compiled for `occ` waves per SIMD (the compiler
     // fits its registers to that), so only the LDS budget is checked here.
-    const int lds = (e.pp ? 3 : 2) * 2 * e.bn * dp * 2;
-    if (lds > kLdsPerCu) return tc;
+    const int lds = (e.wide ? e.nbuf : e.pp ? 3 : 2) * 2 * e.bn * dp * 2;
+    if (lds > kLdsPerCu || !runs_shape(e, n)) return tc;
     const int wg_by_waves = (4 * e.occ) / e.nw;
     const int wg_by_lds = kLdsPerCu / lds;
     const int wg_per_cu = std::max(1, std::min(wg_by_waves, wg_by_lds));
-    const int bm = 32 * e.nw;
+    const int bm = e.bm;
     const int64_t nmb = (n + bm - 1) / bm;
     // workgroups that actually share a CU: fewer tasks than CUs leave each alone
     const int64_t ntask = z * h * nmb;
@@ -252,14 +265,16 @@ int validate_request(int causal, int req_bm, int req_bn) {
 
 // The compiled instantiation nearest to a valid request (log distance in BM
 // and BN; ties go to the larger BN).  This is what RSFA_FLAG_EXACT_TILE runs.
-int resolve_exact(int64_t d, int causal, int dtype, int req_bm, int req_bn, const KernelEntry** out) {
+// n_ctx > 0 leaves out instantiations that cannot run that many keys.
+int resolve_exact(int64_t d, int causal, int dtype, int req_bm, int req_bn, int64_t n_ctx, const KernelEntry** out) {
     const int st = validate_request(causal, req_bm, req_bn);
     if (st != RSFA_OK) return st;
     const KernelEntry* best = nullptr;
     double best_dist = 0.0;
     for_each_kernel([&](const KernelEntry& e) {
         if (e.dtype != dtype || e.d != d || e.causal != (causal ? 1 : 0) || e.mode != MODE_FUSED) return;
-        const double dist = std::fabs(std::log2((double)(32 * e.nw) / req_bm)) + std::fabs(std::log2((double)e.bn / req_bn));
+        if (n_ctx > 0 && !runs_shape(e, n_ctx)) return;
+        const double dist = std::fabs(std::log2((double)e.bm / req_bm)) + std::fabs(std::log2((double)e.bn / req_bn));
         if (!best || dist < best_dist - 1e-9 || (std::fabs(dist - best_dist) <= 1e-9 && e.bn > best->bn)) {
             best = &e;
             best_dist = dist;
@@ -371,9 +386,9 @@ int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype, int32_t
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
     if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
     const KernelEntry* e = nullptr;
-    const int st = resolve_exact(head_dim, causal, dtype, req_block_m, req_block_n, &e);
+    const int st = resolve_exact(head_dim, causal, dtype, req_block_m, req_block_n, 0, &e);
     if (st != RSFA_OK) return st;
-    *block_m = 32 * e->nw;
+    *block_m = e->bm;
     *block_n = e->bn;
     return RSFA_OK;
 }
@@ -388,7 +403,7 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     const KernelEntry* e = nullptr;
     const int st = choose_tiling(z, h, n_ctx, head_dim, causal, dtype, planning_cus(), &e);
     if (st != RSFA_OK) return st;
-    *block_m = 32 * e->nw;
+    *block_m = e->bm;
     *block_n = e->bn;
     return RSFA_OK;
 }
@@ -454,11 +469,11 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // unless RSFA_FLAG_EXACT_TILE asks for the nearest compiled one.
     const KernelEntry* e = nullptr;
     if ((a->flags & RSFA_FLAG_EXACT_TILE) && (a->block_m != 0 || a->block_n != 0))
-        st = resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, &e);
+        st = resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, a->n_ctx, &e);
     else
         st = choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, num_cus, &e);
     if (st != RSFA_OK) return st;
-    const int bm = 32 * e->nw;
+    const int bm = e->bm;
 
     FwdParams p{};
     p.q = a->q;
@@ -514,7 +529,8 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     const int modes[2] = {split ? MODE_PREFIX : MODE_FUSED, MODE_DIAG};
     const int launches = split ? 2 : 1;
     for (int li = 0; li < launches; ++li) {
-        const KernelEntry* k = find_kernel(a->dtype, (int)a->head_dim, e->bn, e->nw, causal ? 1 : 0, modes[li]);
+        const KernelEntry* k = modes[li] == MODE_FUSED ? e
+                               : find_kernel(a->dtype, (int)a->head_dim, e->bn, e->bm, causal ? 1 : 0, modes[li]);
         if (!k) return RSFA_E_TILE;
         const int wgs = resident_wgs(ds, *k);
         int64_t grid = (int64_t)num_cus * wgs;

@@ -158,3 +158,19 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
     msg = lib.rsfa_strerror(_native.E_WORKSPACE).decode()
     assert "rsfa_v8_workspace_bytes" in msg and "rsfa_split_workspace_bytes" in msg
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("N", [64, 1024])
+def test_pipelined_tile_within_the_rounding_bound(N):
+    """The float8 V path on the software-pipelined kernel (tile (256, 32))."""
+    Z, H, D = 1, 4, 128
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + 3)
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, False, 0.1, BM=256, BN=32, exact_tile=True)
+    heads = [(0, 0), (0, H - 1)]
+    exact = A.reference_attention(q, k, v8.float(), False, 0.1, heads=heads)
+    bound = A.fp8v_error_bound(q, k, v8, False, 0.1, heads=heads)
+    got = torch.stack([o[z, h] for z, h in heads])
+    assert torch.isfinite(got).all()
+    excess = ((got - exact).abs() - bound).max().item()
+    assert excess <= 0, f"outside the bound by {excess}"

@@ -332,3 +332,31 @@ def test_many_heads_short_rows(causal):
     heads = [(0, 0), (1023, 17), (Z - 1, H - 1)]
     ref = A.reference_attention(q, k, v, causal, 0.2, heads=heads)
     _assert_close(torch.stack([out[z, h] for z, h in heads]), ref, "many heads")
+
+
+@pytest.mark.parametrize("N", [32, 64, 96, 288, 1024, 2048])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_pipelined_tile_256x32(N, dtype):
+    """The software-pipelined kernel (tile (256, 32): 8 waves of 32 rows, the
+    softmax of key tile t+1 interleaved with the MFMAs of tile t+2 and t, one
+    barrier per pair of key tiles), D=128 non-causal, with its LSE, against the
+    oracle.  N covers one key tile, the two- and three-step tails and the
+    steady loop."""
+    Z, H, D = 2, 3, 128
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + 7, dtype=dtype)
+    print(f"pipelined (256,32): N={N} {dtype}", flush=True)
+    out, lse = F.forward(*_to_gpu(q, k, v), False, 0.3, 256, 32, exact_tile=True, return_lse=True)
+    ref, ref_lse = A.reference_attention(q, k, v, False, 0.3, return_lse=True)
+    _assert_close(out, ref, f"pipelined N={N}")
+    assert (lse.cpu() - ref_lse).abs().max().item() < 1e-2
+
+
+@pytest.mark.parametrize("scale", [-0.4, 0.0, 2.0])
+def test_pipelined_tile_scales_and_strides(scale):
+    """Negative, zero and large scales (frequent rescales of O) on the
+    pipelined kernel, with BSHD-strided inputs."""
+    Z, H, N, D = 2, 4, 512, 128
+    q, k, v = A.make_inputs(Z, H, N, D, seed=99)
+    qd, kd, vd = (t.transpose(1, 2).contiguous().transpose(1, 2).to(DEV) for t in (q, k, v))
+    out = F.forward(qd, kd, vd, False, scale, 256, 32, exact_tile=True)
+    _assert_close(out, A.reference_attention(q, k, v, False, scale), f"pipelined scale={scale}")
