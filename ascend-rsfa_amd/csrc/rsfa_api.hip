@@ -29,6 +29,7 @@ constexpr int kQueues = 8;              // task queues per launch (one per XCD)
 constexpr int kTicketStrideWords = 16;  // one 64-byte line per counter
 constexpr int kSlotWords = kQueues * kTicketStrideWords;
 constexpr int kLdsPerCu = 160 * 1024;   // gfx950
+constexpr int kMaxKernels = 512;        // instantiations in all kernel lists
 
 KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256(),
                           kernels_wide()};
@@ -60,7 +61,8 @@ struct DeviceState {
     int num_cus = 0;              // 0 until queried
     uint32_t* tickets = nullptr;  // kTicketSlots counters, allocated by the first dynamic launch
     std::unordered_map<void*, int> stream_slot;
-    std::unordered_map<const void*, int> occupancy;  // kernel -> resident workgroups per CU
+    std::atomic<int> occupancy[kMaxKernels] = {};  // by kernel_index: resident workgroups per CU, 0 = not yet queried
+    void* scratch = nullptr;                        // this device's address of `scratch` (no-allocation entry point)
 };
 
 DeviceState g_dev[kMaxDevices];
@@ -146,13 +148,27 @@ int32_t queue_count(int64_t num_heads, int64_t grid) {
     return kQueues;
 }
 
+// Position of an instantiation in the kernel lists (a fixed-size cache index).
+int kernel_index(const KernelEntry& e) {
+    int base = 0;
+    for (const KernelList& l : all_lists) {
+        if (&e >= l.entries && &e < l.entries + l.count) return base + (int)(&e - l.entries);
+        base += l.count;
+    }
+    return -1;
+}
+
+// Resident workgroups per CU of an instantiation, queried once per device
+// (a fixed array, so launches allocate no host memory either).
 int resident_wgs(DeviceState& ds, const KernelEntry& e) {
-    std::lock_guard<std::mutex> lock(ds.mu);
-    auto it = ds.occupancy.find(e.fn);
-    if (it != ds.occupancy.end()) return it->second;
+    const int idx = kernel_index(e);
+    if (idx >= 0 && idx < kMaxKernels) {
+        const int cached = ds.occupancy[idx].load(std::memory_order_relaxed);
+        if (cached > 0) return cached;
+    }
     int nb = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, e.fn, e.nw * 64, 0) != hipSuccess || nb <= 0) nb = 1;
-    ds.occupancy.emplace(e.fn, nb);
+    if (idx >= 0 && idx < kMaxKernels) ds.occupancy[idx].store(nb, std::memory_order_relaxed);
     return nb;
 }
 
