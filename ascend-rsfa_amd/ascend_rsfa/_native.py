@@ -9,7 +9,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "librsfa.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # rsfa_status
 OK = 0
@@ -23,6 +23,7 @@ E_DEVICE = -7
 E_LAUNCH = -8
 E_ABI = -9
 E_WORKSPACE = -10
+E_SCRATCH = -11
 
 # rsfa_dtype
 DTYPE_F16 = 0
@@ -33,6 +34,9 @@ DTYPE_F16_V8E5M2 = 2  # q, k, o float16; v float8_e5m2
 FLAG_STATIC_SCHEDULE = 0x1
 FLAG_CAUSAL_SPLIT = 0x2
 FLAG_EXACT_TILE = 0x4
+
+# rsfa_attention_fwd_noalloc's fixed workspace
+NOALLOC_WORKSPACE_BYTES = 16 << 20
 
 # Every symbol include/rsfa.h declares, with (restype, argtypes).
 _I64 = ctypes.c_int64
@@ -71,6 +75,7 @@ class FwdArgs(ctypes.Structure):
 
 SIGNATURES = {
     "rsfa_attention_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
+    "rsfa_attention_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "rsfa_split_workspace_bytes": (ctypes.c_uint64, [_I64, _I64, _I64, _I64, _I32]),
     "rsfa_v8_workspace_bytes": (ctypes.c_uint64, [_I64, _I64, _I64, _I64]),
     "rsfa_get_tiling": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I32, _I32, _PI32, _PI32]),

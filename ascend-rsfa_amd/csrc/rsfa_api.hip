@@ -21,6 +21,14 @@
 #include "kernel_table.hpp"
 
 namespace rsfa {
+
+// The no-allocation entry point's buffer: queue counters in the first 4 KiB,
+// then the workspace.  Host code never uses this name as an address (on the
+// host it only stands for the symbol): rsfa_attention_fwd_noalloc looks the
+// device address up once per device with hipGetSymbolAddress.
+constexpr size_t kScratchCounterBytes = 4096;
+static __device__ __align__(256) char scratch[kScratchCounterBytes + RSFA_NOALLOC_WORKSPACE_BYTES];
+
 namespace {
 
 constexpr int kMaxDevices = 64;
@@ -28,6 +36,7 @@ constexpr int kTicketSlots = 256;       // concurrent streams with a dynamic que
 constexpr int kQueues = 8;              // task queues per launch (one per XCD)
 constexpr int kTicketStrideWords = 16;  // one 64-byte line per counter
 constexpr int kSlotWords = kQueues * kTicketStrideWords;
+static_assert(kSlotWords * sizeof(uint32_t) <= kScratchCounterBytes, "the counters fit the scratch head");
 constexpr int kLdsPerCu = 160 * 1024;   // gfx950
 constexpr int kMaxKernels = 512;        // instantiations in all kernel lists
 
@@ -329,6 +338,13 @@ bool loader_offsets_fit(const KernelEntry& e, int64_t row_stride) {
 // is exact.  One thread per 16 input bytes: x indexes the 16-byte chunks of a
 // head (a row holds 2^lcpr of them, so no division per chunk), y strides over
 // the heads.
+// Zeroes `words` 32-bit words (the no-allocation entry point's queue
+// counters) in stream order; a kernel rather than a memset so that graph
+// capture records a kernel node.
+__global__ void __launch_bounds__(64) clear_words(uint32_t* __restrict__ p, int words) {
+    for (int i = threadIdx.x; i < words; i += blockDim.x) p[i] = 0u;
+}
+
 __global__ void __launch_bounds__(256) widen_v8(const uint8_t* __restrict__ v, int64_t sz, int64_t sh,
                                                 int64_t sn, int32_t h, int32_t nh, int32_t lcpr,
                                                 int64_t per_head, uint32_t* __restrict__ out) {
@@ -378,6 +394,9 @@ const char* rsfa_strerror(int status) {
         case RSFA_E_DEVICE: return "HIP runtime error while preparing the device";
         case RSFA_E_LAUNCH: return "kernel launch failed";
         case RSFA_E_ABI: return "rsfa_fwd_args.struct_size does not match this library";
+        case RSFA_E_SCRATCH:
+            return "the problem needs more workspace (float8 V copy plus split state) than the no-allocation "
+                   "entry point's fixed buffer (RSFA_NOALLOC_WORKSPACE_BYTES)";
         case RSFA_E_WORKSPACE:
             return "workspace missing or smaller than rsfa_v8_workspace_bytes() (float8 V) plus "
                    "rsfa_split_workspace_bytes() (causal split mode)";
@@ -436,10 +455,21 @@ uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t
     return (uint64_t)(2 * z * h * nmb * block_m) * sizeof(float);
 }
 
+// The tile a launch runs: the nearest compiled one for an exact request,
+// otherwise the tile search's choice for `num_cus` CUs (fwd_launch).
+static int launch_tile(const rsfa_fwd_args* a, int num_cus, const KernelEntry** e) {
+    const bool causal = a->causal != 0;
+    if ((a->flags & RSFA_FLAG_EXACT_TILE) && (a->block_m != 0 || a->block_n != 0))
+        return resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, a->n_ctx, e);
+    return choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, num_cus, e);
+}
+
 // Shared body of the launch entry points.  `ws` / `ws_bytes` is the
-// workspace the launch may use (float8 V copy, split state) and `tickets`
-// where its dynamic queue counters live: null lets it take this stream's
-// counter from the library's allocation.
+// workspace the launch may use (float8 V copy, split state).  With
+// `tickets_given`, `tickets` holds the dynamic queue counters (kSlotWords
+// words, cleared here on `stream` before use) and the dynamic schedule is
+// used even under graph capture; otherwise the launch takes this stream's
+// counter from the library's allocation when the stream allows it.
 static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t ws_bytes, uint32_t* tickets,
                       bool tickets_given) {
     if (!a) return RSFA_E_NULL;
@@ -484,11 +514,7 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // the reference: the launch runs the tile the search picks for the shape,
     // unless RSFA_FLAG_EXACT_TILE asks for the nearest compiled one.
     const KernelEntry* e = nullptr;
-    if ((a->flags & RSFA_FLAG_EXACT_TILE) && (a->block_m != 0 || a->block_n != 0))
-        st = resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, a->n_ctx, &e);
-    else
-        st = choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, num_cus, &e);
-    if (st != RSFA_OK) return st;
+    if ((st = launch_tile(a, num_cus, &e)) != RSFA_OK) return st;
     const int bm = e->bm;
 
     FwdParams p{};
@@ -542,6 +568,12 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     }
 
     const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE) && (tickets_given || dynamic_schedule_allowed(stream));
+    if (dynamic && tickets_given) {
+        // caller-placed counters start each call at zero (a launch leaves
+        // them at zero, but the caller's buffer may hold anything)
+        hipLaunchKernelGGL(clear_words, dim3(1), dim3(64), 0, (hipStream_t)stream, tickets, kSlotWords);
+        if (hipGetLastError() != hipSuccess) return RSFA_E_LAUNCH;
+    }
     const int modes[2] = {split ? MODE_PREFIX : MODE_FUSED, MODE_DIAG};
     const int launches = split ? 2 : 1;
     for (int li = 0; li < launches; ++li) {
@@ -560,6 +592,38 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
             return RSFA_E_LAUNCH;
     }
     return RSFA_OK;
+}
+
+int rsfa_attention_fwd_noalloc(const rsfa_fwd_args* a, void* stream) {
+    if (!a) return RSFA_E_NULL;
+    if (a->struct_size != sizeof(rsfa_fwd_args)) return RSFA_E_ABI;
+    // Workspace this call needs, checked before any device work (fwd_launch
+    // repeats every other check).
+    if (valid_dtype(a->dtype) && valid_head_dim(a->head_dim) && a->z >= 1 && a->h >= 1 && a->n_ctx >= 1) {
+        const bool v8 = a->dtype == RSFA_DTYPE_F16_V8E5M2;
+        const bool split = a->causal != 0 && (a->flags & RSFA_FLAG_CAUSAL_SPLIT);
+        uint64_t need = v8 ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
+        if (split) {
+            const KernelEntry* e = nullptr;
+            if (launch_tile(a, planning_cus(), &e) == RSFA_OK)
+                need += rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, e->bm);
+        }
+        if (need > RSFA_NOALLOC_WORKSPACE_BYTES) return RSFA_E_SCRATCH;
+    }
+    int dev = 0, st;
+    if ((st = current_device(&dev)) != RSFA_OK) return st;
+    DeviceState& ds = g_dev[dev];
+    {
+        // set-up, once per device, with that device current
+        std::lock_guard<std::mutex> lock(ds.mu);
+        if (!ds.scratch) {
+            void* ptr = nullptr;
+            if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return RSFA_E_DEVICE;
+            ds.scratch = ptr;
+        }
+    }
+    char* const base = (char*)ds.scratch;
+    return fwd_launch(a, stream, base + kScratchCounterBytes, RSFA_NOALLOC_WORKSPACE_BYTES, (uint32_t*)base, true);
 }
 
 int rsfa_attention_fwd(const rsfa_fwd_args* a, void* stream) {

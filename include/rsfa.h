@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define RSFA_ABI_VERSION 3
+#define RSFA_ABI_VERSION 4
 
 typedef enum rsfa_status {
     RSFA_OK          = 0,
@@ -58,8 +58,10 @@ typedef enum rsfa_status {
     RSFA_E_DEVICE    = -7,  /* HIP runtime error while querying or preparing    */
     RSFA_E_LAUNCH    = -8,  /* kernel launch failed                             */
     RSFA_E_ABI       = -9,  /* struct_size does not match this library          */
-    RSFA_E_WORKSPACE = -10  /* split mode or a float8 V without a large enough
+    RSFA_E_WORKSPACE = -10, /* split mode or a float8 V without a large enough
                                workspace                                        */
+    RSFA_E_SCRATCH   = -11  /* rsfa_attention_fwd_noalloc: the problem needs
+                               more workspace than RSFA_NOALLOC_WORKSPACE_BYTES */
 } rsfa_status;
 
 typedef enum rsfa_dtype {
@@ -120,6 +122,26 @@ typedef struct rsfa_fwd_args {
 /* Fused FlashAttention-2 forward: o = softmax(q k^T * sm_scale [+ causal mask]) v.
  * Replaces _attention.forward (flash_attention_forward.py:547-616). */
 int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
+
+/* Workspace rsfa_attention_fwd_noalloc has for a float8 V copy and the split
+ * state (its fixed per-device buffer holds 4 KiB of queue counters besides). */
+#define RSFA_NOALLOC_WORKSPACE_BYTES (16u << 20)
+
+/* rsfa_attention_fwd without any allocation.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as rsfa_attention_fwd, except that
+ * `workspace`/`workspace_bytes` are ignored: the queue counters and the
+ * workspace (a float8 V's fp16 copy, the split state) live in one fixed
+ * buffer per device, a static device array of RSFA_NOALLOC_WORKSPACE_BYTES
+ * + 4 KiB that the device holds until the process ends.  Problems that need
+ * more workspace fail with RSFA_E_SCRATCH before any device work.  The first
+ * call on a device looks the buffer up (hipGetSymbolAddress); every call
+ * clears its counters with a small kernel on `stream` first.  All calls on one
+ * device share the buffer: calls that overlap in time on one device (other
+ * streams, concurrent graph replays) race and must be serialised by the
+ * caller. */
+int rsfa_attention_fwd_noalloc(const rsfa_fwd_args *args, void *stream);
 
 /* Bytes of fp32 workspace RSFA_FLAG_CAUSAL_SPLIT needs for this problem and
  * tiling (the reference allocates state[2, Z, H, NBM, BM] at 501; this library

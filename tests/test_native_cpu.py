@@ -40,7 +40,7 @@ def test_abi_version_and_struct_layout():
 
 def test_strerror_covers_all_codes():
     lib = _native.lib()
-    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11]
     msgs = [lib.rsfa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(codes)
     assert "unknown" in lib.rsfa_strerror(-99).decode()
