@@ -17,7 +17,7 @@ fp16, copied to the GPU; their SHA-256 is compared with the committed
 fingerprints (tests/golden/input_fingerprints.json) where one exists.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
-                    [--calibrate-copy-mib M]
+                    [--calibrate-copy-mib M] [--device-warmup-s S]
 
 ``--calibrate-copy-mib M`` adds one plain device-to-device copy of M MiB after
 the timed work; under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives
@@ -246,6 +246,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="time only this config name")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0)
+    ap.add_argument("--device-warmup-s", type=float, default=DEVICE_WARMUP_S,
+                    help="seconds of back-to-back launches before the first config (0 under counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the path shards by (batch, head) with no "
@@ -266,7 +268,7 @@ def main():
     for i, cfg in enumerate(configs):
         keep = i == 0 and not args.no_cpu
         results[cfg[0]], kept = time_config(F, torch, cfg, args.steps, args.warmup,
-                                            device_warmup_s=DEVICE_WARMUP_S if i == 0 else 0.0, keep_cpu=keep)
+                                            device_warmup_s=args.device_warmup_s if i == 0 else 0.0, keep_cpu=keep)
         if keep:
             head_inputs = kept
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
@@ -296,7 +298,7 @@ def main():
                    "layout": "[B,H,S,D]", "tiling": r["tiling"], "parallelism": "single GPU"},
         "pct_peak": r["pct_peak"],
         "roofline": roofline(cfg, r),
-        "device_warmup_s": DEVICE_WARMUP_S,
+        "device_warmup_s": args.device_warmup_s,
         "configs": results,
     }
     if CAUSAL_TARGET in results and cfg[0] != CAUSAL_TARGET:
