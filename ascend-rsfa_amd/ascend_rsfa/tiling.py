@@ -31,6 +31,7 @@ Command line::
 
     python -m ascend_rsfa.tiling --cases baseline --output tiling.json \
         [--cache cache.json] [--warmup 5] [--iters 20]
+    python -m ascend_rsfa.tiling --reference-tilings [--output rows.json]
 """
 import argparse
 import json
@@ -227,6 +228,80 @@ def search_case(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16, sm_scale=0.5
     }
 
 
+# The tiles a reference user passes for its 12 cases: the reference's own
+# get_tiling table (flash_attention_forward.py:652-663).
+REFERENCE_TILINGS = {1: (128, 64), 2: (64, 64), 3: (128, 64), 4: (64, 64), 5: (128, 64), 6: (128, 64),
+                     7: (128, 256), 8: (64, 256), 9: (128, 256), 10: (64, 256), 11: (128, 256), 12: (128, 512)}
+
+
+def compare_reference_tilings(warmup=2, iters=5, sm_scale=0.5, rounds=6, verbose=False):
+    """The reference's 12 cases timed three ways on this GPU.
+
+    * ``ours``: ``attention(..., *get_tiling(...))``, this build's choice;
+    * ``ref_hint``: ``attention(..., BM, BN)`` with the reference's tile for
+      the case, the call a reference user makes (the request is a hint, so it
+      runs the tile of ``get_tiling`` as well);
+    * ``ref_exact``: ``forward(..., BM, BN, exact_tile=True)``, the compiled
+      tile nearest to the reference's request forced.
+
+    Inputs: Q, K, V ~ N(0, 0.5^2) in fp16 drawn on the GPU (seed 7 + case),
+    sm_scale 0.5, as the reference's benchmark harness uses
+    (benchmarks/run_correctness_test.py:119-126).  Each time is the median of
+    ``rounds`` interleaved rounds of ``iters`` calls.  Returns one record per
+    case.
+    """
+    from .flash_attention_forward import attention, forward, get_tiling, resolve_tiling
+
+    device = torch.device("cuda", torch.cuda.current_device())
+    rows = []
+    for idx, Z, H, N, D, causal, dtype in REFERENCE_CASES:
+        g = torch.Generator(device=device)
+        g.manual_seed(7 + idx)
+        q, k, v = (torch.randn((Z, H, N, D), generator=g, device=device).mul_(0.5).to(dtype) for _ in range(3))
+        ref_tile = REFERENCE_TILINGS[idx]
+        ours = tuple(get_tiling(Z, H, N, D, causal, dtype))
+        exact = tuple(resolve_tiling(D, causal, *ref_tile, dtype=dtype))
+        runs = {
+            "ours": lambda: attention(q, k, v, causal, sm_scale, *ours),
+            "ref_hint": lambda: attention(q, k, v, causal, sm_scale, *ref_tile),
+            "ref_exact": lambda: forward(q, k, v, causal, sm_scale, *ref_tile, exact_tile=True),
+        }
+        fl = 4.0 * Z * H * N * N * D * (0.5 if causal else 1.0)
+        rec = {"case": idx, "Z": Z, "H": H, "N_CTX": N, "HEAD_DIM": D, "causal": causal,
+               "ref_tile": list(ref_tile), "ours_tile": list(ours), "ref_exact_tile": list(exact)}
+        for name, fn in runs.items():
+            o = fn()
+            torch.cuda.synchronize(device)
+            if not bool(torch.isfinite(o).all()):
+                raise RuntimeError(f"case {idx}: {name} gave non-finite output")
+        # about a second of launches first (the clocks settle under load), then
+        # the three runs interleaved, the order reversed every round; medians
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 1.0:
+            for fn in runs.values():
+                fn()
+            torch.cuda.synchronize(device)
+        times = {name: [] for name in runs}
+        order = list(runs)
+        for r in range(rounds):
+            for name in (order if r % 2 == 0 else order[::-1]):
+                times[name].append(_timer_ms(runs[name], warmup, iters, device))
+        for name in runs:
+            ms = sorted(times[name])[len(times[name]) // 2]
+            rec[name + "_ms"] = round(ms, 4)
+            rec[name + "_tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+        rec["ref_exact_vs_ours"] = round(rec["ref_exact_ms"] / rec["ours_ms"], 3)
+        rec["ref_hint_vs_ours"] = round(rec["ref_hint_ms"] / rec["ours_ms"], 3)
+        rows.append(rec)
+        if verbose:
+            print(f"case {idx:02d} Z={Z} H={H} N={N} D={D} {'causal' if causal else 'non-causal'}: "
+                  f"ours {ours} {rec['ours_ms']:.3f} ms | ref hint {ref_tile} {rec['ref_hint_ms']:.3f} ms | "
+                  f"ref exact {exact} {rec['ref_exact_ms']:.3f} ms", flush=True)
+        del q, k, v
+        torch.cuda.empty_cache()
+    return rows
+
+
 def _key(Z, H, N_CTX, HEAD_DIM, causal, dtype):
     return f"{int(Z)},{int(H)},{int(N_CTX)},{int(HEAD_DIM)},{int(bool(causal))},{str(dtype).replace('torch.', '')}"
 
@@ -299,10 +374,18 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--sm-scale", type=float, default=0.5)
+    ap.add_argument("--reference-tilings", action="store_true",
+                    help="time the reference's 12 cases with the reference's tiles against get_tiling's")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("the search times the GPU kernels: no GPU visible", file=sys.stderr)
         return 2
+    if args.reference_tilings:
+        rows = compare_reference_tilings(args.warmup, args.iters, args.sm_scale, verbose=True)
+        if args.output:
+            with open(args.output, "w") as f:
+                json.dump(rows, f, indent=1)
+        return 0
     cases = []
     if args.cases in ("baseline", "all"):
         cases += list(BASELINE_CASES)

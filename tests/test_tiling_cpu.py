@@ -188,3 +188,14 @@ def faf_model(Z, H, N, D, causal):
         return faf.get_tiling(Z, H, N, D, causal)
     finally:
         tiling.use_cache(saved)
+
+
+def test_reference_tilings_cover_the_reference_cases_and_are_valid_requests():
+    # the tiles of the reference's get_tiling table for its 12 cases
+    # (flash_attention_forward.py:652-663), as the comparison runs them
+    assert sorted(tiling.REFERENCE_TILINGS) == [c[0] for c in tiling.REFERENCE_CASES]
+    for idx, Z, H, N, D, causal, dtype in tiling.REFERENCE_CASES:
+        bm, bn = tiling.REFERENCE_TILINGS[idx]
+        assert (bm, bn) == ((64 if D == 256 else 128), 64) if causal else bn >= 256
+        rbm, rbn = faf.resolve_tiling(D, causal, bm, bn)
+        assert rbm >= 64 and rbn >= 32 and (rbn <= rbm or not causal)
