@@ -35,6 +35,16 @@ round_e5m2 / reference_attention_fp8v / fp8v_error_bound
     exactly; a two-key case (p = 1 and 0.6, 0.6 rounds to 0.625) tells the
     unrounded row sum (O = 0.625 / 1.6) from a rounded one (0.625 / 1.625).
 
+reference_lse_rounded_p
+    The row normalisation of this build's fp16/bf16 kernels: the row sum adds
+    P rounded to the input dtype (the P that enters P.V), so each output row's
+    weights sum to 1; the reference adds the unrounded P (217, 467).  The two
+    differ by at most one rounding of P (2^-11 fp16, 2^-8 bf16 relative).
+    Pinned by (tests/test_oracle.py): two keys with p = 1 and 0.6 give
+    ln(1.60009765625) for fp16 and ln(1.6015625) for bf16 (0.6 rounded),
+    against ln(1.6) for the reference's unrounded sum; and it stays within
+    that rounding bound of reference_attention's LSE on random inputs.
+
 blockwise_attention
     The reference's tiled algorithm with its rounding points (fp16 P, fp16
     round trip of the unnormalised prefix accumulator, -1e6 additive mask,
@@ -169,6 +179,24 @@ def fp8v_error_bound(q, k, v8, causal, sm_scale, heads=None):
     b = b + 2.0 ** -10 * exact.abs() + 1e-4
     b = b.float()
     return b.reshape(q.shape) if heads is None else b
+
+
+def reference_lse_rounded_p(q, k, causal, sm_scale, heads=None):
+    """Row logsumexp as this build's fp16/bf16 kernels normalise: the row sum
+    adds P = exp(S - max S) rounded to the input dtype (the P that enters
+    P.V), where the reference adds the unrounded P
+    (flash_attention_forward.py:217, 467; ``reference_attention(...,
+    return_lse=True)``).  Exact row max (every P <= 1); float64 result
+    [len(heads), N] (all heads when ``heads`` is None, reshaped to [Z, H, N])."""
+    qf, kf, _, hs = _heads_f32(q, k, k, heads)
+    s = torch.matmul(qf, kf.transpose(-1, -2)) * float(sm_scale)
+    if causal:
+        s.masked_fill_(causal_mask(s.shape[-1]), float("-inf"))
+    s = s.double()
+    m = s.max(dim=-1, keepdim=True).values
+    p = torch.exp(s - m).float().to(q.dtype).double()
+    lse = (torch.log(p.sum(dim=-1, keepdim=True)) + m).squeeze(-1)
+    return lse.reshape(q.shape[:3]) if heads is None else lse
 
 
 def brute_force_attention_f64(q, k, v, causal, sm_scale):

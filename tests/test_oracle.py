@@ -5,6 +5,7 @@ needs an Ascend NPU, so the oracle is pinned by independent computations and by
 mathematics: float64 brute-force fixtures, torch's SDPA in float64, closed
 forms, invariants, and planted mistakes that each of these must catch.
 """
+import math
 import os
 
 import numpy as np
@@ -233,3 +234,32 @@ def test_input_fingerprints_cover_the_baseline_configs_and_match_c1():
     q2, k2, v2 = A.make_inputs(*c1["shape"], c1["seed"] + 1)
     assert A.fingerprint(q2, k2, v2) != c1["sha256"]
     assert A.fingerprint(q, v, k) != c1["sha256"]
+
+
+@pytest.mark.parametrize("dtype,p1r", [(torch.float16, 0.60009765625), (torch.bfloat16, 0.6015625)])
+def test_rounded_p_lse_known_answer(dtype, p1r):
+    # two keys whose scores differ by ln(0.6): P = (1, 0.6) unrounded, (1, 0.6 rounded) as the kernels sum it
+    d = 16
+    q = torch.zeros(1, 1, 2, d)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, 1, 2, d)
+    k[0, 0, 1, 0] = 1.0
+    scale = math.log(0.6)  # s = (0, ln 0.6) for both query rows
+    assert torch.equal(q.to(dtype).float(), q) and torch.equal(k.to(dtype).float(), k)
+    lse_r = A.reference_lse_rounded_p(q.to(dtype), k.to(dtype), False, scale)
+    assert abs(lse_r[0, 0, 0].item() - math.log(1.0 + p1r)) < 1e-7
+    _, lse_u = A.reference_attention(q.to(dtype), k.to(dtype), k.to(dtype), False, scale, return_lse=True)
+    assert abs(lse_u[0, 0, 0].item() - math.log(1.6)) < 1e-6
+    # the two normalisations differ by more than the tests' LSE tolerance
+    assert abs(math.log(1.0 + p1r) - math.log(1.6)) > 5e-5
+
+
+@pytest.mark.parametrize("dtype,rel", [(torch.float16, 2.0 ** -11), (torch.bfloat16, 2.0 ** -8)])
+def test_rounded_p_lse_within_one_rounding_of_the_reference(dtype, rel):
+    q, k, v = A.make_inputs(1, 2, 96, 32, seed=12, dtype=dtype)
+    for causal in (False, True):
+        lse_r = A.reference_lse_rounded_p(q, k, causal, 0.4)
+        _, lse_u = A.reference_attention(q, k, v, causal, 0.4, return_lse=True)
+        diff = (lse_r - lse_u.double()).abs().max().item()
+        assert diff <= rel * 1.01 + 1e-6, diff
+        assert diff > 0.0

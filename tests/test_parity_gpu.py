@@ -360,3 +360,33 @@ def test_pipelined_tile_scales_and_strides(scale):
     qd, kd, vd = (t.transpose(1, 2).contiguous().transpose(1, 2).to(DEV) for t in (q, k, v))
     out = F.forward(qd, kd, vd, False, scale, 256, 32, exact_tile=True)
     _assert_close(out, A.reference_attention(q, k, v, False, scale), f"pipelined scale={scale}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_row_sum_adds_the_rounded_p(dtype):
+    """fp16/bf16 kernels divide by the sum of the rounded P (the P that enters
+    P.V), a documented departure from the reference's unrounded sum
+    (flash_attention_forward.py:217, 467).  Row i scores 0 on key 0, a_i on
+    key 1 and -30 elsewhere, so its LSE is ln(1 + p_i) with p_i = e^{a_i}
+    rounded or not; the fp32 LSE tells the two apart."""
+    N, D = 64, 16
+    q = torch.zeros(1, 1, N, D)
+    k = torch.zeros(1, 1, N, D)
+    q[0, 0, :, 0] = torch.linspace(-1.0, -0.05, N)
+    q[0, 0, :, 1] = 1.0
+    k[0, 0, 1, 0] = 1.0
+    k[0, 0, 2:, 1] = -30.0
+    v = torch.randn(1, 1, N, D, generator=torch.Generator().manual_seed(5))
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    print(f"rounded-P row sum: dtype={dtype}", flush=True)
+    _, lse = F.forward(q.cuda(), k.cuda(), v.cuda(), False, 1.0, return_lse=True)
+    torch.cuda.synchronize()
+    got = lse.cpu()[0, 0].double()
+    want = A.reference_lse_rounded_p(q, k, False, 1.0)[0, 0]
+    _, lse_u = A.reference_attention(q, k, v, False, 1.0, return_lse=True)
+    other = lse_u[0, 0].double()
+    assert (got - want).abs().max().item() < 2e-6
+    sep = (want - other).abs()
+    assert sep.max().item() > 2e-5  # the inputs tell the two normalisations apart
+    sel = sep > 1e-5
+    assert bool(((got - want).abs()[sel] < (got - other).abs()[sel]).all())
