@@ -330,10 +330,12 @@ __device__ __forceinline__ void wait_loads_and_sync() {
 // Whether an instantiation runs the ping-pong schedule (8-wave workgroups,
 // three K/V buffers within the 160 KB of LDS of a CU).  At D = 256 (32-key
 // tiles) O^T and Q^T take 192 of the 256 VGPRs: the loop still fits, a few
-// loop-invariant values spill to scratch outside it; it runs non-causal only
-// (measured +2 % there, -2 to +1 % causal).
+// loop-invariant values spill to scratch outside it (+2 % non-causal); causal
+// D = 256 runs only its mask-free tiles in ping-pong, the diagonal in the
+// one-phase loop (+1.9 % on B=64 S=1024; the diagonal's bias blocks there
+// spilled 164 bytes per lane inside the loop).
 constexpr bool uses_pingpong(int d, int bn, int nw, bool causal, int mode) {
-    return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && (d <= 128 || (d == 256 && !causal)) &&
+    return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && (d <= 128 || d == 256) &&
            3 * (2 * bn * (d < 32 ? 32 : d) * 2) <= 160 * 1024 - 64;
 }
 
@@ -370,8 +372,8 @@ fa_fwd_kernel(FwdParams p) {
     // query block: the first S^T MFMA of each 32-key sub-tile accumulates onto
     // a per-wave bias block (0 below the wave's rows, -inf above, triangular
     // on its diagonal), so masking costs no VALU work per score.  Two
-    // sub-tiles per tile (32 VGPRs).
-    constexpr bool DIAG_PP = CAUSAL && PP && NKT <= 2;
+    // sub-tiles per tile (32 VGPRs); at D <= 128 only (register budget).
+    constexpr bool DIAG_PP = CAUSAL && PP && NKT <= 2 && D <= 128;
 
     __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
     __shared__ int s_ticket;
