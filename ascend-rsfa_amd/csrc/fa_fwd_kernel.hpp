@@ -331,9 +331,9 @@ __device__ __forceinline__ void wait_loads_and_sync() {
 // three K/V buffers within the 160 KB of LDS of a CU).  At D = 256 (32-key
 // tiles) O^T and Q^T take 192 of the 256 VGPRs: the loop still fits, a few
 // loop-invariant values spill to scratch outside it (+2 % non-causal); causal
-// D = 256 runs only its mask-free tiles in ping-pong, the diagonal in the
-// one-phase loop (+1.9 % on B=64 S=1024; the diagonal's bias blocks there
-// spilled 164 bytes per lane inside the loop).
+// D = 256 runs its diagonal tiles in the loop too, masked by VALU selects
+// (bias blocks there spilled 164 bytes per lane inside the loop): +3 % on
+// B=64 S=1024 against the one-phase loop.
 constexpr bool uses_pingpong(int d, int bn, int nw, bool causal, int mode) {
     return RSFA_PINGPONG && nw == 8 && mode == MODE_FUSED && (d <= 128 || d == 256) &&
            3 * (2 * bn * (d < 32 ? 32 : d) * 2) <= 160 * 1024 - 64;
@@ -374,6 +374,10 @@ fa_fwd_kernel(FwdParams p) {
     // on its diagonal), so masking costs no VALU work per score.  Two
     // sub-tiles per tile (32 VGPRs); at D <= 128 only (register budget).
     constexpr bool DIAG_PP = CAUSAL && PP && NKT <= 2 && D <= 128;
+    // At D = 256 the diagonal tiles run in the ping-pong loop too, masked by
+    // VALU selects in the softmax phase (no bias registers; at D = 256 the
+    // softmax phase is the short one).
+    constexpr bool DIAG_VM = CAUSAL && PP && !DIAG_PP;
 
     __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
     __shared__ int s_ticket;
@@ -524,7 +528,7 @@ fa_fwd_kernel(FwdParams p) {
         // The first loads go out before the Q loads, so their latencies overlap.
         int jpp = j0;
         if constexpr (PP) jpp = min(j1, (CAUSAL ? m0 : n) / BN);
-        if constexpr (DIAG_PP) {
+        if constexpr (DIAG_PP || DIAG_VM) {
             if (m0 + BM <= n) jpp = j1;  // the diagonal tiles too (whole tiles only)
         }
         if (jpp > j0) {
@@ -570,6 +574,21 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) cb_fill(kt, cb_rel(j0, kt));
         }
+        // DIAG_VM: scores of tile tt a wave's row does not see become -inf
+        // (sub-tiles past the diagonal whole, the diagonal one triangular)
+        auto vmask = [&](f32x16 (&sacc)[NKT], int tt) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                const int rel = cb_rel(tt, kt);
+                if (rel >= 0) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int kk = 8 * (i >> 2) + 4 * hh + (i & 3);  // key of register i in the sub-tile
+                        if (rel > 0 || kk > l32) sacc[kt][i] = -INFINITY;
+                    }
+                }
+            }
+        };
 
         const int srow = bh * p.nmb * BM + m0 + wave * 32 + l32;  // split-state row
         if (MODE == MODE_DIAG) {
@@ -886,6 +905,7 @@ fa_fwd_kernel(FwdParams p) {
                     phase_barrier();  // Y_t
                     prio_valu();
                     x8 pk[NKT][2];
+                    if constexpr (DIAG_VM) vmask(sacc, t);
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     if constexpr (DIAG_PP) {
@@ -908,6 +928,7 @@ fa_fwd_kernel(FwdParams p) {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
                     x8 pk[NKT][2];
+                    if constexpr (DIAG_VM) vmask(sacc, t);
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // its PV
