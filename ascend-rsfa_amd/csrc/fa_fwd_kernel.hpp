@@ -339,6 +339,15 @@ constexpr bool uses_pingpong(int d, int bn, int nw, bool causal, int mode) {
            3 * (2 * bn * (d < 32 ? 32 : d) * 2) <= 160 * 1024 - 64;
 }
 
+// Whether a ping-pong instantiation stages Q through a Q buffer in LDS (the
+// BM = 32*NW query rows of a task beside the three K/V buffers, D = 64 and
+// 128).  Its Q loads use the K/V loader's per-lane 32-bit offsets, which span
+// BN rows of Q.
+constexpr bool uses_q_buffer(int d, int bn, int nw, bool causal, int mode) {
+    return uses_pingpong(d, bn, nw, causal, mode) && d >= 64 && d <= 128 && (32 * nw) % bn == 0 &&
+           3 * (2 * bn * d * 2) + 32 * nw * d * 2 <= 160 * 1024;
+}
+
 template <class T, int D, int BN, int NW, bool CAUSAL, int MODE, int OCC>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 fa_fwd_kernel(FwdParams p) {
@@ -378,11 +387,32 @@ fa_fwd_kernel(FwdParams p) {
     // VALU selects in the softmax phase (no bias registers; at D = 256 the
     // softmax phase is the short one).
     constexpr bool DIAG_VM = CAUSAL && PP && !DIAG_PP;
+    // Q through LDS (ping-pong tiles, D = 64 and 128): a Q buffer after the
+    // K/V buffers takes a task's BM query rows in the K tile layout, filled by
+    // the same coalesced direct loads as K and read into the Q^T registers with
+    // the K operand's reads.  Loaded straight into registers, every load
+    // instruction of Q touches 32 rows (measured: ~5k of the ~9k cycles from a
+    // task's start to its first MFMA).  A task that runs its key loop in
+    // ping-pong also loads the next task's Q into the buffer during two of its
+    // MFMA phases, so that task starts with its Q in LDS.
+    constexpr int QTILE = BM * DP * 2;  // bytes of the Q buffer
+    constexpr bool QPF = uses_q_buffer(D, BN, NW, CAUSAL, MODE);
+    static_assert(!QPF || (NBUF == 3 && NBUF * BUF + QTILE <= 160 * 1024), "Q buffer past the LDS");
 
-    __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF];
-    __shared__ int s_ticket;
+    __shared__ __attribute__((aligned(1024))) char smem_raw[NBUF * BUF + (QPF ? QTILE : 0)];
     RSFA_LDS char* const smem = (RSFA_LDS char*)smem_raw;
     const uint32_t smem_addr = (uint32_t)(uintptr_t)smem;
+    // Ticket broadcast slot.  With the Q buffer the LDS is full: the slot is
+    // then the last word of the third K/V buffer (its V tile), which the
+    // epilogue's staging does not reach, the tiles past the ping-pong loop do
+    // not use, and the loop first loads two barriers after its first phase.
+    RSFA_LDS int* tslot;
+    if constexpr (QPF) {
+        tslot = (RSFA_LDS int*)(smem + NBUF * BUF - 4);
+    } else {
+        __shared__ int s_ticket;
+        tslot = (RSFA_LDS int*)&s_ticket;
+    }
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -423,6 +453,12 @@ fa_fwd_kernel(FwdParams p) {
         kgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.k_sn + cg * 32 + ld_chl * 8) * 2);
         vgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.v_sn + cg * 32 + ld_chl * 8) * 2);
     }
+    // Q rows (QPF): each wave loads its own 32 rows, i.e. the slices of the two
+    // 16-row blocks 2*wave, 2*wave+1 of the Q buffer; the lane's offset inside a
+    // slice is the same for all of them.
+    constexpr int QSPB = CPR / 4;   // 1-KB slices per 16-row block
+    constexpr int NQD = 2 * QSPB;   // Q direct loads per wave
+    const uint32_t qlo = QPF ? (uint32_t)((ld_rib * p.q_sm + ld_chl * 8) * 2) : 0u;
 
     const float c = p.c;
     const int qsign = p.neg ? (int)0x80008000u : 0;
@@ -435,16 +471,31 @@ fa_fwd_kernel(FwdParams p) {
     uint32_t* const ctr = p.ticket ? p.ticket + 16 * qu.x : nullptr;
     int t;
     if (ctr) {
-        if (tid == 0) s_ticket = (int)atomicAdd(ctr, 1u);
+        if (tid == 0) *tslot = (int)atomicAdd(ctr, 1u);
         __syncthreads();
-        t = s_ticket;
+        t = *tslot;
+        if constexpr (QPF) __syncthreads();  // read before the first task writes the slot again
     } else {
         t = qu.rank;
     }
+    bool qready = false;  // QPF: the previous task loaded this task's Q into the Q buffer
 
     while (t < qu.ntask) {
         int nxt = 0;
-        if (ctr && tid == 0) nxt = (int)atomicAdd(ctr, 1u);
+        if (ctr && tid == 0) {
+            if constexpr (QPF) {
+                // from asm, so the compiler adds no wait for it before its use
+                // (the ticket slot write after the first phase's partial load
+                // wait, which covers it: it is the task's oldest vector memory
+                // operation; the epilogue waits for every load)
+                asm volatile("s_nop 4\n\tglobal_atomic_add %0, %1, %2, %3 sc0"
+                             : "=v"(nxt)
+                             : "v"(0u), "v"(1u), "s"(ctr)
+                             : "memory");
+            } else {
+                nxt = (int)atomicAdd(ctr, 1u);
+            }
+        }
 
         int bh, mb;
         decode_task<CAUSAL>(p, qu, t, bh, mb);
@@ -531,8 +582,29 @@ fa_fwd_kernel(FwdParams p) {
         if constexpr (DIAG_PP || DIAG_VM) {
             if (m0 + BM <= n) jpp = j1;  // the diagonal tiles too (whole tiles only)
         }
+        // QPF: direct load q (< NQD) of this wave's rows into the Q buffer, for
+        // the BM rows from qsrc on: block 2*wave + q / QSPB, chunk group q % QSPB.
+        // Only this wave reads what it loads there (read_q).
+        auto dma_q = [&](const elem* qsrc, int q) {
+            const int bb = q / QSPB, cg = q % QSPB;
+            // wave-uniform by construction; made explicit for the SGPR operand
+            const uint64_t a = (uint64_t)(uintptr_t)(qsrc + (int64_t)(32 * wave + 16 * bb) * p.q_sm + cg * 32);
+            const uint64_t ua = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(a >> 32)) << 32) |
+                                (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+            dma16((const void*)(uintptr_t)ua, qlo, smem_addr + NBUF * BUF + (2 * wave + bb) * BLK + cg * 1024);
+        };
+        // Where this task's Q comes from (QPF): the Q buffer, filled by the
+        // previous task (qready) or by loads issued here for a ping-pong task
+        // of a whole query block (q_dma, read after the first phase's load
+        // wait), else global memory.
+        const bool q_dma = QPF && !qready && jpp > j0 && m0 + BM <= n;
+        int t_next = -1;         // QPF, ticket queue: the next ticket, read at the first barrier
+        bool qpf_do = false;     // QPF: this task loads the next task's Q into the Q buffer
+        const elem* qnext = qg;  // its first row
         if (jpp > j0) {
             load_k(j0);
+            if (q_dma)
+                for (int q = 0; q < NQD; ++q) dma_q(qb + (int64_t)m0 * p.q_sm, q);
             load_v(j0);
             if (j0 + 1 < jpp) load_k(j0 + 1);
         } else if (j0 < j1) {
@@ -542,14 +614,46 @@ fa_fwd_kernel(FwdParams p) {
         // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
         // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
         x8 qf[KST];
+        auto q_sign = [&]() {
+            if (qsign) {
+                // a real branch (the asm keeps it from being flattened into an
+                // xor with 0), so positive scales do not wait for Q here
+                asm volatile("");
 #pragma unroll
-        for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(qb + (int64_t)qrow_c * p.q_sm + (2 * s + hh) * 8);
-        if (qsign) {
-            // a real branch (the asm keeps it from being flattened into an xor
-            // with 0), so positive scales do not wait for Q here
-            asm volatile("");
+                for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+            }
+        };
+        // QPF: this wave's 32 rows of the Q buffer (32-row sub-tile `wave`),
+        // with the K operand's read pattern
+        auto read_q = [&]() {
+            const uint32_t qa0 = smem_addr + NBUF * BUF + wave * 2 * BLK + koff[0];
+            const uint32_t qa1 = smem_addr + NBUF * BUF + wave * 2 * BLK + koff[1];
+            i32x4 r[KST];
+            static_for<KST>([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                r[s] = lds_read_b128<s * 512>((s & 1) ? qa1 : qa0);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-            for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+            for (int s = 0; s < KST; ++s) {
+                asm volatile("" : "+v"(r[s]));
+                qf[s] = __builtin_bit_cast(x8, r[s]);
+            }
+            q_sign();
+        };
+        if (QPF && qready) {
+            read_q();
+        } else if (!q_dma) {
+#pragma unroll
+            for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(qb + (int64_t)qrow_c * p.q_sm + (2 * s + hh) * 8);
+            // Q has arrived here as far as the compiler knows (the tile loops
+            // wait for the first tile's loads, issued before Q's, anyway):
+            // without this it would wait for Q, i.e. for the newest direct
+            // loads, at every use of qf inside the loops.  Kept on this path:
+            // where the paths join it would make the others wait too.
+#pragma unroll
+            for (int s = 0; s < KST; ++s) asm volatile("" : "+v"(qf[s]));
+            q_sign();
         }
 
         f32x16 o[DT];
@@ -781,12 +885,6 @@ fa_fwd_kernel(FwdParams p) {
             pv_part((uint32_t)(buf * BUF + TILE), nkt_act, pk, masked);
         };
 
-        // Q has arrived by now as far as the compiler knows: the tile loops wait
-        // for the first tile's loads (issued before Q's) anyway, and without
-        // this it would wait for Q, i.e. for the newest direct loads, at
-        // every use of qf inside the loops.
-#pragma unroll
-        for (int s = 0; s < KST; ++s) asm volatile("" : "+v"(qf[s]));
 
         int j = j0;
         if constexpr (PP) {
@@ -849,7 +947,7 @@ fa_fwd_kernel(FwdParams p) {
                 // LDS byte addresses of the buffers of tiles tv, tv + 1, tv + 2
                 // (rotated once per tile instead of computing jj % NBUF)
                 uint32_t b_tv = smem_addr + bofs(j0), b_t1 = smem_addr + bofs(j0 + 1), b_t2 = smem_addr + bofs(j0 + 2);
-                auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT]) {
+                auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT], auto wq, int qi) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
                     static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
@@ -889,19 +987,61 @@ fa_fwd_kernel(FwdParams p) {
                                 }
                             }
                         }
+                        // QPF: half of the next task's Q loads (from load qi on),
+                        // right after the phase's wait for the previous loads
+                        if constexpr (decltype(wq)::value && m == D0 + 1) {
+                            if (qi >= 0) static_for<NQD / 2>([&](auto qc) { dma_q(qnext, qi + decltype(qc)::value); });
+                        }
                     });
                 };
 
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_j0, V_j0, K_j0+1
-                if (grp) phase_barrier();
-                phase_barrier();  // X_j0: QK only, then the loads of K_{j0+2}, V_{j0+1}
+                // K_j0 (and Q): the first phase reads only these; V_j0 and K_j0+1
+                // are waited for at the end of X_j0 (each load_k / load_v is
+                // NSL direct loads per wave, issued in order K_j0, Q, V_j0, K_j0+1)
+                static_assert(NINST % NW == 0, "every wave issues NSL loads per tile");
+                if (j0 + 1 < jpp)
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NSL) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NSL) : "memory");
+                if constexpr (QPF) {
+                    // the next ticket (its atomic is done), published by the barrier
+                    if (ctr && tid == 0) {
+                        asm volatile("" : "+v"(nxt));  // after the wait above
+                        *tslot = nxt;
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
+                if constexpr (QPF) {
+                    if (q_dma) read_q();  // this wave's own loads, waited for above
+                }
+                phase_barrier();  // waves 0-3: X_j0; waves 4-7 wait one phase more
+                if constexpr (QPF) {
+                    // the next task; when this task has at least four ping-pong
+                    // tiles and the next one a whole query block, its Q is loaded
+                    // in the phases X_{j0+2} and X_{j0+3}
+                    const int tn = ctr ? __builtin_amdgcn_readfirstlane(*tslot) : t + qu.nwg;
+                    if (ctr) t_next = tn;
+                    if (tn < qu.ntask && jpp - j0 >= 4) {
+                        int nbh, nmb;
+                        decode_task<CAUSAL>(p, qu, tn, nbh, nmb);
+                        if ((nmb + 1) * BM <= n) {
+                            const int nb = nbh / p.H, nh = nbh - nb * p.H;
+                            qpf_do = true;
+                            qnext = qg + nb * p.q_sz + nh * p.q_sh + (int64_t)nmb * BM * p.q_sm;
+                        }
+                    }
+                }
+                if (grp) phase_barrier();  // X_j0: QK only, then the loads of K_{j0+2}, V_{j0+1}
                 prio_mfma();
                 f32x16 sacc[NKT];
                 qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V_j0, K_j0+1, published by the next barrier
                 if (j0 + 2 < jpp) load_k(j0 + 2);
                 if (j0 + 1 < jpp) load_v(j0 + 1);
                 int t = j0;
-                for (; t + 1 < jpp; ++t) {
+                // one step: Y_t, then X_{t+1} (WQ: with the slots of the Q loads
+                // of the next task, from load qi on when qi >= 0)
+                auto pp_step = [&](auto wq, int qi) {
                     phase_barrier();  // Y_t
                     prio_valu();
                     x8 pk[NKT][2];
@@ -918,12 +1058,21 @@ fa_fwd_kernel(FwdParams p) {
                     }
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
-                    x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc);
+                    x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc, wq, qi);
                     const uint32_t b_old = b_tv;
                     b_tv = b_t1;
                     b_t1 = b_t2;
                     b_t2 = b_old;
+                };
+                if constexpr (QPF) {
+                    // a task that loads the next task's Q (in X_{j0+2} and
+                    // X_{j0+3}) runs its first three steps in a copy with the
+                    // load slots; the loop below carries no check for them
+                    // (a check in every MFMA phase cost more than the loads save)
+                    if (qpf_do)
+                        for (; t < j0 + 3; ++t) pp_step(std::true_type(), t == j0 ? -1 : (t - j0 - 1) * (NQD / 2));
                 }
+                for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1);
                 {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
@@ -933,7 +1082,7 @@ fa_fwd_kernel(FwdParams p) {
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // its PV
                     prio_mfma();
-                    x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc);
+                    x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc, std::false_type(), -1);
                     prio_valu();
                 }
                 if (!grp) phase_barrier();
@@ -968,6 +1117,9 @@ fa_fwd_kernel(FwdParams p) {
         }
 
         // epilogue
+        // (QPF: the next task's Q loads are waited for here, the barrier below
+        // publishes them)
+        if constexpr (QPF) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const float lt = swap_sum(l_sum);
         if (MODE == MODE_PREFIX) {
             if (hh == 0) {
@@ -1040,13 +1192,19 @@ fa_fwd_kernel(FwdParams p) {
 
         if (ctr) {
             __syncthreads();
-            if (tid == 0) s_ticket = nxt;
-            __syncthreads();
-            t = s_ticket;
+            if (QPF && t_next >= 0) {
+                t = t_next;
+            } else {
+                if (tid == 0) *tslot = nxt;
+                __syncthreads();
+                t = *tslot;
+                if constexpr (QPF) __syncthreads();  // read before the next task writes the slot
+            }
         } else {
             __syncthreads();
             t += qu.nwg;
         }
+        qready = qpf_do;
     }
 
     // The workgroup holding the last ticket handed out by its queue returns the

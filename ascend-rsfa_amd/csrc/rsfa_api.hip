@@ -324,8 +324,9 @@ int check_tensor(const void* ptr, const int64_t st[4], int mult = 8) {
     return RSFA_OK;
 }
 
-// The K/V loader of a tile keeps one uniform 64-bit base per tile and per-lane
-// 32-bit byte offsets that span the tile's BN rows: ((BN - 1) * row stride +
+// The K/V loader of a tile (and the Q loader of the ping-pong tiles that stage
+// Q through LDS) keeps one uniform 64-bit base per tile and per-lane 32-bit
+// byte offsets that span the tile's BN rows: ((BN - 1) * row stride +
 // row width) * 2 bytes must stay below 2^32, or the offsets would wrap.
 bool loader_offsets_fit(const KernelEntry& e, int64_t row_stride) {
     const int64_t dp = e.d < 32 ? 32 : e.d;
@@ -497,8 +498,10 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
     const int64_t v_rows = v8 ? a->head_dim : a->v_stride[2];  // a float8 V is read from its fp16 copy
     for_each_kernel([&](const KernelEntry& e) {
+        const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS
         if (st == RSFA_OK && e.dtype == a->dtype && e.d == a->head_dim &&
-            (!loader_offsets_fit(e, a->k_stride[2]) || !loader_offsets_fit(e, v_rows)))
+            (!loader_offsets_fit(e, a->k_stride[2]) || !loader_offsets_fit(e, v_rows) ||
+             (q_loader && !loader_offsets_fit(e, a->q_stride[2]))))
             st = RSFA_E_ALIGN;
     });
     if (st != RSFA_OK) return st;

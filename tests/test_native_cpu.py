@@ -183,6 +183,8 @@ def _valid_args(**over):
     # 32-bit per-lane offsets would wrap, so they are refused before launch
     (dict(k_stride=[0, 0, 16909320, 1]), _native.E_ALIGN),
     (dict(v_stride=[0, 0, 16909320, 1]), _native.E_ALIGN),
+    # Q rows, loaded by the same loader into LDS by the ping-pong tiles
+    (dict(q_stride=[0, 0, 16909320, 1]), _native.E_ALIGN),
     (dict(head_dim=256, k_stride=[0, 0, 69273664, 1]), _native.E_ALIGN),
     # the split state's rows are 32-bit: Z*H*N_CTX (rounded up to 256) < 2^31
     (dict(z=1024, h=1024, n_ctx=2048, causal=1, flags=_native.FLAG_CAUSAL_SPLIT), _native.E_SHAPE),
@@ -202,6 +204,7 @@ def test_attention_fwd_without_gpu_reports_device_error():
 
 @pytest.mark.parametrize("over", [
     dict(k_stride=[0, 0, 16909312, 1]),            # the largest 8-multiple row stride whose 128-row tile fits
+    dict(q_stride=[0, 0, 16909312, 1]),
     dict(head_dim=256, k_stride=[0, 0, 69273656, 1]),
     dict(z=1024, h=1024, n_ctx=2048, causal=1),     # fused causal has no split-state limit
     dict(block_m=128, block_n=64, causal=1),        # a valid request (a hint)
