@@ -27,10 +27,11 @@
  *     never frees them.  Strides are in elements.  The last (head-dim) stride
  *     of q/k/v/o must be 1, every other stride a multiple of 8 elements (16
  *     for a float8 V) and every base pointer 16-byte aligned.  The K and V
- *     row strides must also keep one key tile inside 4 GiB:
- *     ((BLOCK_N - 1) * row_stride + max(D, 32)) * 2 < 2^32 bytes for the
- *     tile that runs (BLOCK_N <= 128: row strides below ~16.9 M elements
- *     always pass).  RSFA_E_ALIGN otherwise.
+ *     row strides (and at D = 64 and 128 the Q row stride, whose rows the
+ *     8-wave tiles load the same way) must also keep BLOCK_N rows inside
+ *     4 GiB: ((BLOCK_N - 1) * row_stride + max(D, 32)) * 2 < 2^32 bytes for
+ *     every tile the call could run (BLOCK_N <= 128: row strides below
+ *     ~16.9 M elements always pass).  RSFA_E_ALIGN otherwise.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t, NULL = the
  *     null stream).  The call returns after the launch, not after completion.
  *   - Return codes: 0 on success, a negative rsfa_status otherwise.  Invalid
