@@ -562,13 +562,16 @@ fa_fwd_kernel(FwdParams p) {
         // Ping-pong buffers: tile jj of K and V in buffer jj % NBUF.
         auto bofs = [&](int jj) { return (uint32_t)((jj % NBUF) * BUF); };
         // slice sl of this wave's share of tile jj of K (or V)
-        auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
+        // (the tile's first row at tp)
+        auto pp_dma_at = [&](const elem* tp, const uint32_t(&go)[NSL], uint32_t dst0, int sl) {
             const int w = sl * NW + wave;
             if (NINST % NW == 0 || w < NINST) {
                 const int cg = ((w * 64) % (16 * CPR)) / 64;
-                if (CPRV == CPR || 4 * cg + ld_chl < CPRV)
-                    dma16(th + (int64_t)(jj * BN) * sn, go[sl], dst0 + w * 1024);
+                if (CPRV == CPR || 4 * cg + ld_chl < CPRV) dma16(tp, go[sl], dst0 + w * 1024);
             }
+        };
+        auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
+            pp_dma_at(th + (int64_t)(jj * BN) * sn, go, dst0, sl);
         };
         auto dma_k = [&](int jj, int sl) { pp_dma(kh, p.k_sn, kgo, jj, smem_addr + bofs(jj), sl); };
         auto dma_v = [&](int jj, int sl) { pp_dma(vh, p.v_sn, vgo, jj, smem_addr + bofs(jj) + TILE, sl); };
@@ -947,6 +950,13 @@ fa_fwd_kernel(FwdParams p) {
                 // LDS byte addresses of the buffers of tiles tv, tv + 1, tv + 2
                 // (rotated once per tile instead of computing jj % NBUF)
                 uint32_t b_tv = smem_addr + bofs(j0), b_t1 = smem_addr + bofs(j0 + 1), b_t2 = smem_addr + bofs(j0 + 2);
+                // first rows of the tiles the next X phase loads (K_{tl+1}, V_tl for
+                // tl = t + 2 at step t), advanced by one tile per step: left to
+                // the compiler, the causal kernels rebuilt them with 64-bit
+                // multiplies at every load, inside the MFMA stream
+                const int64_t kstep = (int64_t)BN * p.k_sn, vstep = (int64_t)BN * p.v_sn;
+                const elem* kld = kh + (j0 + 3) * kstep;
+                const elem* vld = vh + (j0 + 2) * vstep;
                 auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT], auto wq, int qi) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
@@ -981,9 +991,9 @@ fa_fwd_kernel(FwdParams p) {
                                 if constexpr (q == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                                 // tl = tv + 2: K_{tv+3} into the buffer of tile tv, V_{tv+2}
                                 if constexpr (q < NSL) {
-                                    if (tl + 1 < jpp) pp_dma(kh, p.k_sn, kgo, tl + 1, b_tv, q);
+                                    if (tl + 1 < jpp) pp_dma_at(kld, kgo, b_tv, q);
                                 } else {
-                                    if (tl < jpp) pp_dma(vh, p.v_sn, vgo, tl, b_t2 + TILE, q - NSL);
+                                    if (tl < jpp) pp_dma_at(vld, vgo, b_t2 + TILE, q - NSL);
                                 }
                             }
                         }
@@ -1059,6 +1069,8 @@ fa_fwd_kernel(FwdParams p) {
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc, wq, qi);
+                    kld += kstep;
+                    vld += vstep;
                     const uint32_t b_old = b_tv;
                     b_tv = b_t1;
                     b_t1 = b_t2;
