@@ -728,7 +728,7 @@ fa_fwd_kernel(FwdParams p) {
         // S^T = K Q^T for the key tile whose K sits at LDS byte offset kofs.
         // Masked: keys past each row's last visible key become -inf, and 32-key
         // sub-tiles at or past nkt_act (no row of the wave sees them) are skipped.
-        auto qk_part = [&](uint32_t kofs, int kbase, int nkt_act, f32x16 (&sacc)[NKT], auto masked) {
+        auto qk_part = [&](uint32_t kofs, int kbase, int nkt_act, f32x16 (&sacc)[NKT], auto masked, auto use_cb) {
             constexpr bool MASK = decltype(masked)::value;
             const RSFA_LDS char* kt_lds = smem + kofs;
             const f32x16 zero = {};  // the first k-step adds to an inline-constant 0
@@ -754,7 +754,7 @@ fa_fwd_kernel(FwdParams p) {
                     constexpr int ahead = (NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1);
                     lgkm_wait<ahead>(ring[i % NB]);
                     sacc[kt] = T::mfma(__builtin_bit_cast(x8, ring[i % NB]), qf[ss],
-                                       ss == 0 ? (DIAG_PP ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
+                                       ss == 0 ? (DIAG_PP && decltype(use_cb)::value ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
                     if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
                 });
             } else {
@@ -883,7 +883,7 @@ fa_fwd_kernel(FwdParams p) {
         auto tile_step = [&](int buf, int kbase, int nkt_act, auto masked) {
             f32x16 sacc[NKT];
             x8 pk[NKT][2];
-            qk_part((uint32_t)(buf * BUF), kbase, nkt_act, sacc, masked);
+            qk_part((uint32_t)(buf * BUF), kbase, nkt_act, sacc, masked, std::false_type());
             softmax_part(sacc, pk, masked);
             pv_part((uint32_t)(buf * BUF + TILE), nkt_act, pk, masked);
         };
@@ -957,7 +957,7 @@ fa_fwd_kernel(FwdParams p) {
                 const int64_t kstep = (int64_t)BN * p.k_sn, vstep = (int64_t)BN * p.v_sn;
                 const elem* kld = kh + (j0 + 3) * kstep;
                 const elem* vld = vh + (j0 + 2) * vstep;
-                auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT], auto wq, int qi) {
+                auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT], auto wq, int qi, auto use_cb) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
                     static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
@@ -979,7 +979,7 @@ fa_fwd_kernel(FwdParams p) {
                             constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
                             lgkm_wait<N>(kr[i % XNB]);
                             sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss],
-                                               ss == 0 ? (DIAG_PP ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
+                                               ss == 0 ? (DIAG_PP && decltype(use_cb)::value ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
                         }
                         if constexpr (m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
                         // load q of NDMA at op D0 + q * DSTEP (q < NDMA: the wave's K
@@ -1044,21 +1044,21 @@ fa_fwd_kernel(FwdParams p) {
                 if (grp) phase_barrier();  // X_j0: QK only, then the loads of K_{j0+2}, V_{j0+1}
                 prio_mfma();
                 f32x16 sacc[NKT];
-                qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free);
+                qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free, std::true_type());
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V_j0, K_j0+1, published by the next barrier
                 if (j0 + 2 < jpp) load_k(j0 + 2);
                 if (j0 + 1 < jpp) load_v(j0 + 1);
                 int t = j0;
                 // one step: Y_t, then X_{t+1} (WQ: with the slots of the Q loads
                 // of the next task, from load qi on when qi >= 0)
-                auto pp_step = [&](auto wq, int qi) {
+                auto pp_step = [&](auto wq, int qi, auto use_cb) {
                     phase_barrier();  // Y_t
                     prio_valu();
                     x8 pk[NKT][2];
                     if constexpr (DIAG_VM) vmask(sacc, t);
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
-                    if constexpr (DIAG_PP) {
+                    if constexpr (DIAG_PP && decltype(use_cb)::value) {
                         // bias of tile t+1 where it changes: onto the diagonal, or past it
 #pragma unroll
                         for (int kt = 0; kt < NKT; ++kt) {
@@ -1068,7 +1068,7 @@ fa_fwd_kernel(FwdParams p) {
                     }
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
-                    x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc, wq, qi);
+                    x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc, wq, qi, use_cb);
                     kld += kstep;
                     vld += vstep;
                     const uint32_t b_old = b_tv;
@@ -1082,9 +1082,20 @@ fa_fwd_kernel(FwdParams p) {
                     // load slots; the loop below carries no check for them
                     // (a check in every MFMA phase cost more than the loads save)
                     if (qpf_do)
-                        for (; t < j0 + 3; ++t) pp_step(std::true_type(), t == j0 ? -1 : (t - j0 - 1) * (NQD / 2));
+                        for (; t < j0 + 3; ++t)
+                            pp_step(std::true_type(), t == j0 ? -1 : (t - j0 - 1) * (NQD / 2), std::true_type());
                 }
-                for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1);
+                if constexpr (DIAG_PP) {
+                    // steps whose key tile lies below the whole query block run
+                    // a copy without the bias blocks (their bias is 0): with
+                    // the 32 bias VGPRs free the softmax phase is ~70 cycles
+                    // shorter; the bias of the next tile is then filled whole
+                    const int jd = m0 / BN;  // first key tile of the diagonal block
+                    for (; t + 1 < jpp && t + 1 < jd; ++t) pp_step(std::false_type(), -1, std::false_type());
+#pragma unroll
+                    for (int kt = 0; kt < NKT; ++kt) cb_fill(kt, cb_rel(t + 1, kt));
+                }
+                for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1, std::true_type());
                 {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
@@ -1094,7 +1105,7 @@ fa_fwd_kernel(FwdParams p) {
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // its PV
                     prio_mfma();
-                    x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc, std::false_type(), -1);
+                    x_phase(std::integral_constant<int, NPV>(), t, -1, pk, sacc, std::false_type(), -1, std::true_type());
                     prio_valu();
                 }
                 if (!grp) phase_barrier();
