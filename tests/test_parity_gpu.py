@@ -247,6 +247,37 @@ def test_q_buffer_task_chains(D, BN, dtype, causal, Z, N):
 
 
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D,tile", [(64, (0, 0)), (64, (256, 128)), (128, (0, 0)), (128, (256, 64)),
+                                    (256, (0, 0)), (256, (256, 32))])
+def test_nan_inputs_propagate_by_row(causal, D, tile):
+    """A NaN score makes its row's output NaN, as in the reference, whose row
+    max propagates NaN (flash_attention_forward.py:200-203) and whose row sum
+    and P.V carry it (:217, :221): a NaN in query row r turns exactly output
+    row r to NaN; a NaN in key row j turns every row that sees key j to NaN
+    (all rows non-causal, rows >= j causal), while causal query blocks that end
+    before key j never load it and stay finite.  Finite rows match the oracle."""
+    Z, H, N, r, j = 1, 2, 1024, 300, 700
+    q, k, v = A.make_inputs(Z, H, N, D, seed=99 + D)
+    q[0, 0, r, 5] = float("nan")
+    k[0, 1, j, 3] = float("nan")
+    scale = 1 / math.sqrt(D)
+    out = F.forward(*_to_gpu(q, k, v), causal, scale, *tile, exact_tile=tile != (0, 0)).float().cpu()
+    bad0 = torch.isnan(out[0, 0]).any(-1)
+    assert bool(torch.isnan(out[0, 0, r]).all()) and int(bad0.sum()) == 1
+    bad1 = torch.isnan(out[0, 1]).any(-1)
+    if causal:
+        assert bool(bad1[j:].all()) and not bool(bad1[:512].any())  # blocks of <= 256 rows ending by row 512
+    else:
+        assert bool(bad1.all())
+    ref = A.reference_attention(q, k, v, causal, scale)
+    keep0 = torch.ones(N, dtype=torch.bool)
+    keep0[r] = False
+    _assert_close(out[0, 0, keep0], ref[0, 0, keep0], f"D={D} tile={tile} causal={causal} head 0")
+    if causal:
+        _assert_close(out[0, 1, :512], ref[0, 1, :512], f"D={D} tile={tile} causal head 1 rows < 512")
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_dynamic_and_static_schedules_bitwise_equal(causal):
     q, k, v = A.make_inputs(4, 8, 1024, 128, seed=15)
     qd, kd, vd = _to_gpu(q, k, v)
