@@ -426,6 +426,19 @@ fa_fwd_kernel(FwdParams p) {
     uint32_t koff[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) koff[e] = (l32 >> 4) * BLK + hh * 256 + ((l16 ^ (8 * e + 4 * hh)) * 16);
+    // At D = 256 (O^T and Q^T hold 192 of the 256 VGPRs) values the compiler
+    // hoists out of the task loop are spilled, and each reload from scratch
+    // makes it wait for every load in flight (vmcnt(0)): at a task's start the
+    // K/V loads, then Q's, went out one latency at a time.  REG_TIGHT kernels
+    // recompute what the start needs per task instead (+1.2 to +3.8 % on
+    // D = 256 shapes); the lane id is then taken from asm (v_mbcnt), which
+    // the compiler cannot hoist.
+    constexpr bool REG_TIGHT = D > 128;
+    auto fresh_lane = []() {
+        int ln;
+        asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+        return ln;
+    };
     // V (A operand of O^T via transposing reads): lane l16 of a 16-lane group
     // addresses row (l16/4) of the group's 4 keys and columns 4*(l16%4)..+3 of
     // its 16 head dims; the hardware hands lane j column j of the 4 rows.
@@ -501,10 +514,12 @@ fa_fwd_kernel(FwdParams p) {
         decode_task<CAUSAL>(p, qu, t, bh, mb);
         const int b = bh / p.H;
         const int h = bh - b * p.H;
-        const int n = p.n_ctx;
+        // REG_TIGHT: opaque per task, so values derived from n stay inside the
+        // task instead of being hoisted out of the task loop and spilled
+        int n = p.n_ctx;
+        if constexpr (REG_TIGHT) asm volatile("" : "+s"(n));
         const int m0 = mb * BM;
         const int qrow = m0 + wave * 32 + l32;
-        const int qrow_c = min(qrow, n - 1);
 
         const elem* qb = qg + b * p.q_sz + h * p.q_sh;
         const elem* kh = kg + b * p.k_sz + h * p.k_sh;
@@ -614,16 +629,29 @@ fa_fwd_kernel(FwdParams p) {
             load_tile(j0, 0);
         }
 
+        // first element of this lane's Q fragments, q[qrow][8hh]
+        auto q_lane = [&]() {
+            if constexpr (REG_TIGHT) {
+                const int ln = fresh_lane();
+                return qb + (int64_t)min(m0 + wave * 32 + (ln & 31), n - 1) * p.q_sm + ((ln >> 5) & 1) * 8;
+            } else {
+                return qb + (int64_t)min(qrow, n - 1) * p.q_sm + hh * 8;
+            }
+        };
         // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
         // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
         x8 qf[KST];
         auto q_sign = [&]() {
-            if (qsign) {
+            int qs = qsign;
+            // REG_TIGHT: tested here, in an SGPR (hoisted out of the task loop,
+            // the test was kept in a VGPR and spilled)
+            if constexpr (REG_TIGHT) asm volatile("" : "+s"(qs));
+            if (qs) {
                 // a real branch (the asm keeps it from being flattened into an
                 // xor with 0), so positive scales do not wait for Q here
                 asm volatile("");
 #pragma unroll
-                for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qsign);
+                for (int s = 0; s < KST; ++s) qf[s] = __builtin_bit_cast(x8, __builtin_bit_cast(i32x4, qf[s]) ^ qs);
             }
         };
         // QPF: this wave's 32 rows of the Q buffer (32-row sub-tile `wave`),
@@ -647,8 +675,9 @@ fa_fwd_kernel(FwdParams p) {
         if (QPF && qready) {
             read_q();
         } else if (!q_dma) {
+            const elem* const ql = q_lane();
 #pragma unroll
-            for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(qb + (int64_t)qrow_c * p.q_sm + (2 * s + hh) * 8);
+            for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(ql + 16 * s);
             // Q has arrived here as far as the compiler knows (the tile loops
             // wait for the first tile's loads, issued before Q's, anyway):
             // without this it would wait for Q, i.e. for the newest direct

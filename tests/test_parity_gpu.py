@@ -221,7 +221,7 @@ def test_noncausal_many_and_few_tasks(D, dtype, Z, H, N):
         assert (lse[b, h] - ref_lse[i]).abs().max().item() < 1e-3
 
 
-@pytest.mark.parametrize("D,BN", [(64, 128), (128, 64)])
+@pytest.mark.parametrize("D,BN", [(64, 128), (128, 64), (256, 32)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("Z,N", [(4, 300), (2, 1000), (2, 1792)])
@@ -229,15 +229,17 @@ def test_q_buffer_task_chains(D, BN, dtype, causal, Z, N):
     """The 8-wave ping-pong tiles at D = 64 and 128 stage Q through an LDS
     buffer, load the next task's Q into it while the current task runs (when
     the current task has at least four ping-pong key tiles and the next one a
-    whole query block) and pass the next ticket through the third K/V buffer.
-    More tasks than workgroups (320-560 tasks), whole and partial last query
-    blocks, key loops shorter and longer than four tiles; every head against
-    the oracle, and the static grid-stride order (other task chains) bitwise
-    equal to the dynamic queue."""
+    whole query block) and pass the next ticket through the third K/V buffer;
+    at D = 256 (no Q buffer) each task loads its Q into registers, with the
+    addresses its start needs recomputed per task.  More tasks than workgroups
+    (320-560 tasks), whole and partial last query blocks, key loops shorter
+    and longer than four tiles, a negative scale (sign flip of Q after it is
+    read) at N = 1000; every head against the oracle, and the static
+    grid-stride order (other task chains) bitwise equal to the dynamic queue."""
     H = 40
     q, k, v = A.make_inputs(Z, H, N, D, seed=7 * N + D, dtype=dtype)
     qd, kd, vd = _to_gpu(q, k, v)
-    scale = 1 / math.sqrt(D)
+    scale = (-1.0 if N == 1000 else 1.0) / math.sqrt(D)
     a = F.forward(qd, kd, vd, causal, scale, 256, BN, exact_tile=True)
     b = F.forward(qd, kd, vd, causal, scale, 256, BN, exact_tile=True, static_schedule=True)
     torch.cuda.synchronize()
