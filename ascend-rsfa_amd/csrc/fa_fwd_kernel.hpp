@@ -329,8 +329,8 @@ __device__ __forceinline__ void wait_loads_and_sync() {
 
 // Whether an instantiation runs the ping-pong schedule (8-wave workgroups,
 // three K/V buffers within the 160 KB of LDS of a CU).  At D = 256 (32-key
-// tiles) O^T and Q^T take 192 of the 256 VGPRs: the loop still fits, a few
-// loop-invariant values spill to scratch outside it (+2 % non-causal); causal
+// tiles) O^T and Q^T take 192 of the 256 VGPRs: the loop still fits (+2 %
+// non-causal against the one-phase loop); causal
 // D = 256 runs its diagonal tiles in the loop too, masked by VALU selects
 // (bias blocks there spilled 164 bytes per lane inside the loop): +3 % on
 // B=64 S=1024 against the one-phase loop.
