@@ -58,6 +58,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // How far (in log2 units) the running row max may lag the true max before the
 // accumulator is rescaled.  P = 2^(s*c - m) stays <= 2^15, inside the normal
@@ -69,7 +70,9 @@ constexpr float RESCALE_SLACK = 15.0f;
 
 struct TypeF16 {
     static constexpr bool p8 = false;  // P rounded to the input dtype
+    static constexpr bool v8 = false;  // V tiles in LDS as float8 bytes
     typedef _Float16 elem;
+    typedef _Float16 velem;  // element of V in global memory
     typedef _Float16 x8 __attribute__((ext_vector_type(8)));
     typedef _Float16 x4 __attribute__((ext_vector_type(4)));
     typedef _Float16 x2 __attribute__((ext_vector_type(2)));
@@ -91,7 +94,9 @@ struct TypeF16 {
 
 struct TypeBF16 {
     static constexpr bool p8 = false;
+    static constexpr bool v8 = false;
     typedef __bf16 elem;
+    typedef __bf16 velem;
     typedef __bf16 x8 __attribute__((ext_vector_type(8)));
     typedef __bf16 x4 __attribute__((ext_vector_type(4)));
     typedef __bf16 x2 __attribute__((ext_vector_type(2)));
@@ -124,6 +129,20 @@ struct TypeF16P8 : TypeF16 {
         const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
         // ... become the high bytes of two fp16
         return __builtin_bit_cast(x2, ((w << 8) & 0xFF00u) | ((w << 16) & 0xFF000000u));
+    }
+};
+
+// TypeF16P8 without the fp16 copy of V (head dim 128): V's tiles go into LDS
+// as the e5m2 bytes themselves (half the bytes of the copy), P is rounded to
+// e5m2 bytes, and P.V runs on the float8 MFMA (e5m2 x e5m2, 64 keys per MFMA,
+// twice the fp16 rate).  Its products are exact in fp32, as the fp16 MFMA's
+// are on the widened operands, and it accumulates in fp32.
+struct TypeF16V8 : TypeF16P8 {
+    static constexpr bool v8 = true;
+    typedef uint8_t velem;
+    static __device__ __forceinline__ f32x16 mfma8(i32x8 a, i32x8 b, f32x16 c) {
+        // cbsz = blgp = 1: both operands bf8 (e5m2); no block scale
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 0, 0, 0);
     }
 };
 
@@ -291,10 +310,46 @@ __device__ __forceinline__ i32x2 lds_read_tr16(uint32_t addr) {
     return r;
 }
 
+template <int OFF>
+__device__ __forceinline__ i32x2 lds_read_tr8(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "DS offset is 16 bits");
+    i32x2 r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFF));
+    return r;
+}
+
+// Eight e5m2 bytes (byte e = element e) as eight fp16: the fp16 with the value
+// of an e5m2 byte b has the bits b << 8 (same sign, exponent bias and width,
+// two more mantissa bits), so the widening is exact.
+// One v_perm_b32 per two elements: selector byte k picks byte k of the 64-bit
+// {0, w} (0-3: w) or, as 0x0C, a zero byte.
+__device__ __forceinline__ i32x4 widen_e5m2x8(i32x2 r) {
+    const uint32_t lo = (uint32_t)r[0], hi = (uint32_t)r[1];
+    return (i32x4){(int)__builtin_amdgcn_perm(0u, lo, 0x010C000Cu), (int)__builtin_amdgcn_perm(0u, lo, 0x030C020Cu),
+                   (int)__builtin_amdgcn_perm(0u, hi, 0x010C000Cu), (int)__builtin_amdgcn_perm(0u, hi, 0x030C020Cu)};
+}
+
+// The float8 P.V MFMA's operands: A from four byte-transposing reads (8
+// bytes each), B from the P bytes of two 32-key sub-tiles (16 each).
+__device__ __forceinline__ i32x8 cat4(i32x2 r0, i32x2 r1, i32x2 r2, i32x2 r3) {
+    return (i32x8){r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+template <class X8>
+__device__ __forceinline__ i32x8 cat2(X8 p0, X8 p1) {
+    const i32x4 b0 = __builtin_bit_cast(i32x4, p0), b1 = __builtin_bit_cast(i32x4, p1);
+    return (i32x8){b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+}
+
 template <int N, class V>
 __device__ __forceinline__ void lgkm_wait(V& v) {
     static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+
+template <int N, class V>
+__device__ __forceinline__ void lgkm_wait4(V& a, V& b, V& c, V& d) {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
 }
 
 template <int N, class V>
@@ -313,12 +368,19 @@ __device__ __forceinline__ void phase_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// LDS reads still outstanding once the reads of op m of an operand stream have
-// completed, when ops [0, min(m + pf, nops)) have been issued and ops below npv
-// take two reads each, the others one.
-constexpr int x_reads_after(int npv, int nops, int pf, int m) {
+// An operand stream of nops ops: ops below npv (P.V) take pvr reads each and
+// are read pfv ops ahead, the others (QK) one read, pf ops ahead (pfv >= pf,
+// so reads go out in op order): op x's reads are issued after op
+// x_issue_after(x) (-1: before the stream).  x_reads_pending: LDS reads still
+// outstanding once op m's have completed, at op m's wait.
+constexpr int x_issue_after(int npv, int pf, int pfv, int x) {
+    const int a = x - (x < npv ? pfv : pf);
+    return a < -1 ? -1 : a;
+}
+constexpr int x_reads_pending(int npv, int nops, int pf, int pfv, int pvr, int m) {
     int n = 0;
-    for (int q = m + 1; q < m + pf && q < nops; ++q) n += q < npv ? 2 : 1;
+    for (int x = m + 1; x < nops; ++x)
+        if (x_issue_after(npv, pf, pfv, x) <= m - 1) n += x < npv ? pvr : 1;
     return n;
 }
 
@@ -352,6 +414,7 @@ template <class T, int D, int BN, int NW, bool CAUSAL, int MODE, int OCC>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 fa_fwd_kernel(FwdParams p) {
     typedef typename T::elem elem;
+    typedef typename T::velem velem;
     typedef typename T::x8 x8;
     typedef typename T::x4 x4;
     typedef typename T::x2 x2;
@@ -364,9 +427,17 @@ fa_fwd_kernel(FwdParams p) {
     constexpr int NKT = BN / 32;         // 32-key sub-tiles of a key tile
     constexpr int BM = NW * 32;
     constexpr int BLK = 32 * DP;          // bytes of a 16-row block
-    constexpr int TILE = BN * DP * 2;     // bytes of one K (or V) tile
-    constexpr int BUF = 2 * TILE;         // K + V
+    constexpr int TILE = BN * DP * 2;     // bytes of one K (or fp16 V) tile
     constexpr int NINST = BN * CPR / 64;  // 1-KB direct loads per tile
+    // V8: V tiles of e5m2 bytes, BN rows of D bytes; the 1-KB slice s holds
+    // rows 8s..8s+7 whole, and row R keeps its 16-byte chunk c at position
+    // c ^ (R % 4 + 4 * ((R / 8) % 2)), so the eight rows one transposing read
+    // of P.V gathers (below) sit in eight different chunk columns.
+    constexpr bool V8 = T::v8;
+    static_assert(!V8 || (D == 128 && BN % 64 == 0), "byte V tiles: head dim 128, 64-key groups");
+    constexpr int TILEV = V8 ? BN * D : TILE;  // bytes of one V tile
+    constexpr int BUF = TILE + TILEV;          // K + V
+    constexpr int NINSTV = V8 ? TILEV / 1024 : NINST;
     static_assert(BN % 32 == 0 && BN >= 32, "BN must be a multiple of 32");
     static_assert(D % 16 == 0, "D must be a multiple of 16");
     static_assert((BN * CPR) % 64 == 0, "tile must be whole 1-KB load slices");
@@ -448,6 +519,23 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
         voff[u] = vcc * 256 + (((8 * u + 4 * hh + (l16 >> 2)) ^ (4 * vcc)) * 16) + 8 * (l16 & 1);
+    // V8 (ds_read_b64_tr_b8): in a 16-lane group lanes 2r and 2r+1 address
+    // bytes 0-7 and 8-15 of row r of eight rows, and the hardware hands lane j
+    // column j of the eight rows.  For the P.V MFMA of 16-key group q' (keys
+    // 16q'.. of the tile) and head-dim block db, operand byte e of lane
+    // (d + 32 hh) must be key 16q' + 4hh + e % 4 + 8 (e / 4), the key whose
+    // rounded P that lane holds in byte slot e of its P^T operand (the S^T
+    // accumulator layout); so row r of the group is that key for e = r, and
+    // the group's 16 columns are head dims 32db + 16((lane / 16) % 2) ...
+    // Offset from the tile at q' = 0 (q' adds 16q' rows), per db.
+    uint32_t vo8[V8 ? DT : 1];
+    if constexpr (V8) {
+        const int tr = l16 >> 1;                                    // row r of the group
+        const int rowb = D * (4 * hh + (tr & 3) + 8 * (tr >> 2)) + 8 * (l16 & 1);
+        const int x = ((lane >> 4) & 1) ^ tr;                       // chunk bit 0 ^ the row's swizzle
+#pragma unroll
+        for (int db = 0; db < DT; ++db) vo8[db] = (uint32_t)(rowb + 16 * (x ^ (2 * db)));
+    }
 
     // Loader: in every 1-KB slice lane i fills chunk 4*cg + i/16 of the 16-row
     // block's row (i%16) ^ 4*((i/16)%4), so its global offset inside the block
@@ -457,14 +545,25 @@ fa_fwd_kernel(FwdParams p) {
     // Byte offsets of this wave's slices (slice w = sl*NW + wave) from the first
     // row of a whole tile, for K and V; the tile loop only adds a uniform base.
     constexpr int NSL = (NINST + NW - 1) / NW;
-    uint32_t kgo[NSL], vgo[NSL];
+    constexpr int NSLV = (NINSTV + NW - 1) / NW;  // V slices per wave
+    uint32_t kgo[NSL], vgo[NSLV];
 #pragma unroll
     for (int sl = 0; sl < NSL; ++sl) {
         const int w = sl * NW + wave;
         const int blk = (w * 64) / (16 * CPR);
         const int cg = ((w * 64) % (16 * CPR)) / 64;
         kgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.k_sn + cg * 32 + ld_chl * 8) * 2);
-        vgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.v_sn + cg * 32 + ld_chl * 8) * 2);
+        if constexpr (!V8) vgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.v_sn + cg * 32 + ld_chl * 8) * 2);
+    }
+    // V8: lane i of slice s fills position i of the slice, i.e. chunk column
+    // i % 8 of row 8s + i / 8, with the row's chunk (i % 8) ^ swizzle
+    auto v8_chunk = [&](int s) { return (lane & 7) ^ ((lane >> 3) & 3) ^ (4 * (s & 1)); };
+    if constexpr (V8) {
+#pragma unroll
+        for (int sl = 0; sl < NSLV; ++sl) {
+            const int s = sl * NW + wave;
+            vgo[sl] = (uint32_t)((8 * s + (lane >> 3)) * p.v_sn + 16 * v8_chunk(s));
+        }
     }
     // Q rows (QPF): each wave loads its own 32 rows, i.e. the slices of the two
     // 16-row blocks 2*wave, 2*wave+1 of the Q buffer; the lane's offset inside a
@@ -477,7 +576,7 @@ fa_fwd_kernel(FwdParams p) {
     const int qsign = p.neg ? (int)0x80008000u : 0;
     const elem* const qg = (const elem*)p.q;
     const elem* const kg = (const elem*)p.k;
-    const elem* const vgp = (const elem*)p.v;
+    const velem* const vgp = (const velem*)p.v;
     elem* const og = (elem*)p.o;
 
     const Queue qu = make_queue<CAUSAL>(p);
@@ -523,7 +622,7 @@ fa_fwd_kernel(FwdParams p) {
 
         const elem* qb = qg + b * p.q_sz + h * p.q_sh;
         const elem* kh = kg + b * p.k_sz + h * p.k_sh;
-        const elem* vh = vgp + b * p.v_sz + h * p.v_sh;
+        const velem* vh = vgp + b * p.v_sz + h * p.v_sh;
         elem* ob = og + b * p.o_sz + h * p.o_sh;
 
         // key tiles of this task
@@ -535,7 +634,7 @@ fa_fwd_kernel(FwdParams p) {
         auto load_tile = [&](int j, int buf) {
             const int kbase = j * BN;
             const elem* kt0 = kh + (int64_t)kbase * p.k_sn;
-            const elem* vt0 = vh + (int64_t)kbase * p.v_sn;
+            const velem* vt0 = vh + (int64_t)kbase * p.v_sn;
             const uint32_t dst0 = smem_addr + buf * BUF;
             if (kbase + BN <= n) {
                 // whole tile: one uniform base per tensor, per-slice offsets precomputed
@@ -546,13 +645,33 @@ fa_fwd_kernel(FwdParams p) {
                         const int cg = ((w * 64) % (16 * CPR)) / 64;
                         if (CPRV == CPR || 4 * cg + ld_chl < CPRV) {
                             dma16(kt0, kgo[sl], dst0 + w * 1024);
-                            dma16(vt0, vgo[sl], dst0 + w * 1024 + TILE);
+                            if constexpr (!V8) dma16(vt0, vgo[sl], dst0 + w * 1024 + TILE);
                         }
+                    }
+                }
+                if constexpr (V8) {
+#pragma unroll
+                    for (int sl = 0; sl < NSLV; ++sl) {
+                        const int s = sl * NW + wave;
+                        if (NINSTV % NW == 0 || s < NINSTV) dma16(vt0, vgo[sl], dst0 + TILE + s * 1024);
                     }
                 }
                 return;
             }
             const int last = n - 1 - kbase;  // last row of the tile inside the sequence
+            if constexpr (V8) {
+                // rows past the sequence re-read its last row (masked later)
+#pragma unroll
+                for (int sl = 0; sl < NSLV; ++sl) {
+                    const int s = sl * NW + wave;
+                    if (NINSTV % NW == 0 || s < NINSTV) {
+                        const int row0 = min(8 * s, last);
+                        const int rr = min(8 * s + (lane >> 3), last) - row0;
+                        const uint32_t vo = (uint32_t)(rr * p.v_sn + 16 * v8_chunk(s));
+                        dma16(vt0 + (int64_t)row0 * p.v_sn, vo, dst0 + TILE + s * 1024);
+                    }
+                }
+            }
 #pragma unroll
             for (int sl = 0; sl < NSL; ++sl) {
                 const int w = sl * NW + wave;
@@ -563,12 +682,13 @@ fa_fwd_kernel(FwdParams p) {
                     const int row0 = min(16 * blk, last);
                     const int rr = min(16 * blk + ld_rib, last) - row0;
                     const uint32_t ko = (uint32_t)((rr * p.k_sn + ld_chl * 8) * 2);
-                    const uint32_t vo = (uint32_t)((rr * p.v_sn + ld_chl * 8) * 2);
                     const elem* ks = kt0 + (int64_t)row0 * p.k_sn + cg * 32;
-                    const elem* vs = vt0 + (int64_t)row0 * p.v_sn + cg * 32;
                     if (CPRV == CPR || 4 * cg + ld_chl < CPRV) {
                         dma16(ks, ko, dst0 + w * 1024);
-                        dma16(vs, vo, dst0 + w * 1024 + TILE);
+                        if constexpr (!V8) {
+                            const uint32_t vo = (uint32_t)((rr * p.v_sn + ld_chl * 8) * 2);
+                            dma16(vt0 + (int64_t)row0 * p.v_sn + cg * 32, vo, dst0 + w * 1024 + TILE);
+                        }
                     }
                 }
             }
@@ -585,13 +705,22 @@ fa_fwd_kernel(FwdParams p) {
                 if (CPRV == CPR || 4 * cg + ld_chl < CPRV) dma16(tp, go[sl], dst0 + w * 1024);
             }
         };
-        auto pp_dma = [&](const elem* th, int64_t sn, const uint32_t(&go)[NSL], int jj, uint32_t dst0, int sl) {
-            pp_dma_at(th + (int64_t)(jj * BN) * sn, go, dst0, sl);
+        // the same for V (dst0: the V tile)
+        auto pp_dma_v_at = [&](const velem* tp, uint32_t dst0, int sl) {
+            const int w = sl * NW + wave;
+            if constexpr (V8) {
+                if (NINSTV % NW == 0 || w < NINSTV) dma16(tp, vgo[sl], dst0 + w * 1024);
+            } else {
+                if (NINST % NW == 0 || w < NINST) {
+                    const int cg = ((w * 64) % (16 * CPR)) / 64;
+                    if (CPRV == CPR || 4 * cg + ld_chl < CPRV) dma16(tp, vgo[sl], dst0 + w * 1024);
+                }
+            }
         };
-        auto dma_k = [&](int jj, int sl) { pp_dma(kh, p.k_sn, kgo, jj, smem_addr + bofs(jj), sl); };
-        auto dma_v = [&](int jj, int sl) { pp_dma(vh, p.v_sn, vgo, jj, smem_addr + bofs(jj) + TILE, sl); };
+        auto dma_k = [&](int jj, int sl) { pp_dma_at(kh + (int64_t)(jj * BN) * p.k_sn, kgo, smem_addr + bofs(jj), sl); };
+        auto dma_v = [&](int jj, int sl) { pp_dma_v_at(vh + (int64_t)(jj * BN) * p.v_sn, smem_addr + bofs(jj) + TILE, sl); };
         auto load_k = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_k(jj, sl); };
-        auto load_v = [&](int jj) { for (int sl = 0; sl < NSL; ++sl) dma_v(jj, sl); };
+        auto load_v = [&](int jj) { for (int sl = 0; sl < NSLV; ++sl) dma_v(jj, sl); };
 
         // [j0, jpp): ping-pong tiles (whole tiles no row of the workgroup masks).
         // The first loads go out before the Q loads, so their latencies overlap.
@@ -843,13 +972,24 @@ fa_fwd_kernel(FwdParams p) {
             constexpr int kt = u / 8, h2 = (u / 4) % 2, i = u % 4;
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i], c, -msub));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * h2 + 2 * i + 1], c, -msub));
-            const x2 pr = T::cvt2(p0, p1);
-            if constexpr (T::p8)
+            if constexpr (V8) {
+                // e5m2 bytes of the float8 P.V MFMA's B operand: the pair's
+                // accumulator registers rho = 8h2 + 2i, +1 of sub-tile kt go to
+                // bytes 16kt + rho (pk[kt][0] holds sub-tile kt's 16 bytes)
+                constexpr int dw = 2 * h2 + (i >> 1);
+                i32x4 w = __builtin_bit_cast(i32x4, pk[kt][0]);
+                w[dw] = __builtin_amdgcn_cvt_pk_bf8_f32(p0, p1, (i & 1) ? w[dw] : 0, (i & 1) != 0);
+                pk[kt][0] = __builtin_bit_cast(x8, w);
                 l_sum += p0 + p1;  // the reference sums the unrounded P for an e5m2 V
-            else
-                l_sum = T::dot2(pr, T::ones2(), l_sum);
-            pk[kt][h2][2 * i] = pr[0];
-            pk[kt][h2][2 * i + 1] = pr[1];
+            } else {
+                const x2 pr = T::cvt2(p0, p1);
+                if constexpr (T::p8)
+                    l_sum += p0 + p1;  // the reference sums the unrounded P for an e5m2 V
+                else
+                    l_sum = T::dot2(pr, T::ones2(), l_sum);
+                pk[kt][h2][2 * i] = pr[0];
+                pk[kt][h2][2 * i + 1] = pr[1];
+            }
         };
         // Online softmax of one S^T tile: row max (softmax_max), then
         // P = exp2(S c - m) rounded to the input type into pk and the row sum
@@ -862,7 +1002,55 @@ fa_fwd_kernel(FwdParams p) {
         auto pv_part = [&](uint32_t vofs, int nkt_act, const x8 (&pk)[NKT][2], auto masked) {
             constexpr bool MASK = decltype(masked)::value;
             const RSFA_LDS char* vt_lds = smem + vofs;
-            if (!MASK) {
+            if constexpr (V8) {
+                // read i = (d*NKT + kt)*2 + h2 fetches keys 16(2kt + h2).. of
+                // head-dim block d (byte-transposing, 8 bytes per lane); every
+                // fourth completes the A operand of a 64-key float8 MFMA, whose
+                // B operand is sub-tiles 2kk, 2kk+1 of the P bytes
+                constexpr int NM = DT * NKT * 2;
+                constexpr int PF = 8;       // two float8 MFMAs ahead
+                constexpr int NB = PF + 4;  // the four reads of an MFMA stay live to it
+                const uint32_t vb = smem_addr + vofs;
+                if (!MASK) {
+                    i32x2 rv[NB];
+                    auto issue = [&](auto ic) {
+                        constexpr int i = decltype(ic)::value;
+                        constexpr int d = i / (2 * NKT), kt = (i / 2) % NKT, h2 = i % 2;
+                        rv[i % NB] = lds_read_tr8<(2 * kt + h2) * 16 * D>(vb + vo8[d]);
+                    };
+                    static_for<PF>(issue);
+                    static_for<NM>([&](auto ic) {
+                        constexpr int i = decltype(ic)::value;
+                        constexpr int d = i / (2 * NKT), qq = i % (2 * NKT);
+                        constexpr int ahead = (NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1);
+                        if constexpr (qq % 4 == 3) {
+                            i32x2 &r0 = rv[(i - 3) % NB], &r1 = rv[(i - 2) % NB], &r2 = rv[(i - 1) % NB], &r3 = rv[i % NB];
+                            lgkm_wait4<ahead>(r0, r1, r2, r3);
+                            o[d] = T::mfma8(cat4(r0, r1, r2, r3), cat2(pk[qq / 2 - 1][0], pk[qq / 2][0]), o[d]);
+                            __builtin_amdgcn_sched_barrier(0);  // issued here, not sunk below the next reads
+                        }
+                        if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
+                    });
+                } else {
+                    // sub-tiles no row of the wave sees (kt >= nkt_act) hold
+                    // P = 0; their V is not read (zeros), as the fp16 path skips them
+#pragma unroll
+                    for (int d = 0; d < DT; ++d)
+#pragma unroll
+                        for (int kk = 0; kk < NKT / 2; ++kk)
+                            if (2 * kk < nkt_act) {
+                                i32x2 r[4];
+#pragma unroll
+                                for (int qq = 0; qq < 4; ++qq) {
+                                    r[qq] = (i32x2){0, 0};
+                                    if (2 * kk + qq / 2 < nkt_act)
+                                        r[qq] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                                            (RSFA_LDS i32x2*)(vt_lds + (4 * kk + qq) * 16 * D + vo8[d]));
+                                }
+                                o[d] = T::mfma8(cat4(r[0], r[1], r[2], r[3]), cat2(pk[2 * kk][0], pk[2 * kk + 1][0]), o[d]);
+                            }
+                }
+            } else if (!MASK) {
                 // MFMA i = (d, kt, h2), i = (d*NKT + kt)*2 + h2, two transposing reads each
                 constexpr int NM = DT * NKT * 2;
                 constexpr int PF = PV_PREFETCH < NM ? PV_PREFETCH : NM;
@@ -956,18 +1144,28 @@ fa_fwd_kernel(FwdParams p) {
                 // uses l_sum before the barrier); at D = 64 the softmax phase is
                 // the longer one (measured: +2 % at D = 128, -5 % at D = 64).
                 constexpr bool LSUM_IN_Y = D >= 128;
-                constexpr int NDMA = 2 * NSL;  // direct loads per wave per X phase
+                constexpr int NDMA = NSL + NSLV;  // direct loads per wave per X phase
                 constexpr int DSTEP = 2;       // MFMAs between them
-                i32x2 rlo[XNB], rhi[XNB];
+                // V8: rlo only, read PFV ahead (two float8 MFMAs; one is
+                // shorter than an LDS read's latency), and the four reads of
+                // a float8 MFMA stay live to it
+                constexpr int PFV = V8 ? 8 : XPF;
+                constexpr int XNBV = V8 ? PFV + 4 : XNB;
+                i32x2 rlo[XNBV], rhi[XNB];
                 i32x4 kr[XNB];
                 uint32_t xa[4];  // V reads (two halves), K reads (even / odd k-steps)
+                uint32_t xv[V8 ? DT : 1];  // V8: V reads per head-dim block
                 auto x_issue = [&](auto mc) {
                     constexpr int m = decltype(mc)::value;
                     if constexpr (m < NPV) {
                         constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
-                        constexpr int off = (2 * kt + h2) * BLK + d * 1024;
-                        rlo[m % XNB] = lds_read_tr16<off>(xa[0]);
-                        rhi[m % XNB] = lds_read_tr16<off>(xa[1]);
+                        if constexpr (V8) {
+                            rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[d]);
+                        } else {
+                            constexpr int off = (2 * kt + h2) * BLK + d * 1024;
+                            rlo[m % XNB] = lds_read_tr16<off>(xa[0]);
+                            rhi[m % XNB] = lds_read_tr16<off>(xa[1]);
+                        }
                     } else {
                         constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
                         kr[i % XNB] = lds_read_b128<kt * 2 * BLK + ss * 512>(xa[2 + (ss & 1)]);
@@ -985,32 +1183,57 @@ fa_fwd_kernel(FwdParams p) {
                 // multiplies at every load, inside the MFMA stream
                 const int64_t kstep = (int64_t)BN * p.k_sn, vstep = (int64_t)BN * p.v_sn;
                 const elem* kld = kh + (j0 + 3) * kstep;
-                const elem* vld = vh + (j0 + 2) * vstep;
+                const velem* vld = vh + (j0 + 2) * vstep;
                 auto x_phase = [&](auto nm, int tv, int tl, const x8(&pk)[NKT][2], f32x16(&sacc)[NKT], auto wq, int qi, auto use_cb) {
                     constexpr int M = decltype(nm)::value;
                     constexpr int D0 = M - NDMA * DSTEP;
                     static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
-                    xa[0] = b_tv + TILE + voff[0];
-                    xa[1] = b_tv + TILE + voff[1];
+                    if constexpr (V8) {
+#pragma unroll
+                        for (int d = 0; d < DT; ++d) xv[d] = b_tv + TILE + vo8[d];
+                    } else {
+                        xa[0] = b_tv + TILE + voff[0];
+                        xa[1] = b_tv + TILE + voff[1];
+                    }
                     xa[2] = b_t1 + koff[0];
                     xa[3] = b_t1 + koff[1];
-                    static_for<(XPF < M ? XPF : M)>(x_issue);
+                    static_for<M>([&](auto xc) {
+                        constexpr int x = decltype(xc)::value;
+                        if constexpr (x_issue_after(NPV, XPF, PFV, x) == -1) x_issue(xc);
+                    });
                     const f32x16 zero = {};
                     static_for<M>([&](auto mc) {
                         constexpr int m = decltype(mc)::value;
-                        constexpr int N = x_reads_after(NPV, M, XPF, m);
+                        constexpr int N = x_reads_pending(NPV, M, XPF, PFV, V8 ? 1 : 2, m);
                         if constexpr (m < NPV) {
-                            constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
-                            lgkm_wait2<N>(rlo[m % XNB], rhi[m % XNB]);
-                            const i32x2 lo = rlo[m % XNB], hi = rhi[m % XNB];
-                            o[d] = T::mfma(__builtin_bit_cast(x8, (i32x4){lo[0], lo[1], hi[0], hi[1]}), pk[kt][h2], o[d]);
+                            if constexpr (V8) {
+                                // read m = (d*NKT + kt)*2 + h2; every fourth ends
+                                // a 64-key float8 MFMA (as in pv_part), which
+                                // waits for its four reads
+                                constexpr int d = m / (2 * NKT), qq = m % (2 * NKT);
+                                if constexpr (qq % 4 == 3) {
+                                    i32x2 &r0 = rlo[(m - 3) % XNBV], &r1 = rlo[(m - 2) % XNBV], &r2 = rlo[(m - 1) % XNBV],
+                                          &r3 = rlo[m % XNBV];
+                                    lgkm_wait4<N>(r0, r1, r2, r3);
+                                    o[d] = T::mfma8(cat4(r0, r1, r2, r3), cat2(pk[qq / 2 - 1][0], pk[qq / 2][0]), o[d]);
+                                    // issued here, not sunk below the next reads and waits
+                                    __builtin_amdgcn_sched_barrier(0);
+                                }
+                            } else {
+                                constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
+                                lgkm_wait2<N>(rlo[m % XNB], rhi[m % XNB]);
+                                const i32x2 lo = rlo[m % XNB], hi = rhi[m % XNB];
+                                o[d] = T::mfma(__builtin_bit_cast(x8, (i32x4){lo[0], lo[1], hi[0], hi[1]}), pk[kt][h2], o[d]);
+                            }
                         } else {
                             constexpr int i = m - NPV, ss = i / NKT, kt = i % NKT;
                             lgkm_wait<N>(kr[i % XNB]);
                             sacc[kt] = T::mfma(__builtin_bit_cast(x8, kr[i % XNB]), qf[ss],
                                                ss == 0 ? (DIAG_PP && decltype(use_cb)::value ? cb[DIAG_PP ? kt : 0] : zero) : sacc[kt]);
                         }
-                        if constexpr (m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
+                        // the next reads: a P.V op PFV ahead, or a QK op XPF ahead
+                        if constexpr (m + PFV < NPV) x_issue(std::integral_constant<int, m + PFV>());
+                        if constexpr (m + XPF >= NPV && m + XPF < M) x_issue(std::integral_constant<int, m + XPF>());
                         // load q of NDMA at op D0 + q * DSTEP (q < NDMA: the wave's K
                         // slices, then its V slices)
                         if constexpr (m >= D0 && m < D0 + NDMA * DSTEP && (m - D0) % DSTEP == 0) {
@@ -1022,7 +1245,7 @@ fa_fwd_kernel(FwdParams p) {
                                 if constexpr (q < NSL) {
                                     if (tl + 1 < jpp) pp_dma_at(kld, kgo, b_tv, q);
                                 } else {
-                                    if (tl < jpp) pp_dma_at(vld, vgo, b_t2 + TILE, q - NSL);
+                                    if (tl < jpp) pp_dma_v_at(vld, b_t2 + TILE, q - NSL);
                                 }
                             }
                         }
@@ -1036,12 +1259,12 @@ fa_fwd_kernel(FwdParams p) {
 
                 // K_j0 (and Q): the first phase reads only these; V_j0 and K_j0+1
                 // are waited for at the end of X_j0 (each load_k / load_v is
-                // NSL direct loads per wave, issued in order K_j0, Q, V_j0, K_j0+1)
-                static_assert(NINST % NW == 0, "every wave issues NSL loads per tile");
+                // NSL (NSLV) direct loads per wave, issued in order K_j0, Q, V_j0, K_j0+1)
+                static_assert(NINST % NW == 0 && NINSTV % NW == 0, "every wave issues NSL (NSLV) loads per tile");
                 if (j0 + 1 < jpp)
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NSL) : "memory");
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NSLV + NSL) : "memory");
                 else
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NSL) : "memory");
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NSLV) : "memory");
                 if constexpr (QPF) {
                     // the next ticket (its atomic is done), published by the barrier
                     if (ctr && tid == 0) {

@@ -11,5 +11,6 @@ using namespace rsfa;
         RSFA_TILE_ENTRIES(T, DTYPE, 128, 64, 4, 2)
 #endif
 
+// float8 V at head dim 128: V's bytes go into LDS as they are (TypeF16V8)
 RSFA_DEFINE_KERNEL_LIST(kernels_d128, RSFA_D128_TILES(TypeF16, 0), RSFA_D128_TILES(TypeBF16, 1),
-                        RSFA_D128_TILES(TypeF16P8, 2))
+                        RSFA_D128_TILES(TypeF16V8, 2))

@@ -1,5 +1,6 @@
 // Instantiations of the one-wave-per-SIMD forward kernel (fa_fwd_wide.hpp):
-// head dim 128, non-causal, fp16, bf16 and fp16 with a float8 e5m2 V.
+// head dim 128, non-causal, fp16 and bf16 (a float8 V at head dim 128 is read
+// as bytes, which only fa_fwd_kernel's TypeF16V8 tiles do).
 //
 // Built with -mllvm -amdgpu-mfma-vgpr-form=1 (build_native.py): with 512
 // registers per wave the compiler would otherwise give every MFMA an AGPR
@@ -17,8 +18,7 @@ using namespace rsfa;
 #endif
 
 #if RSFA_WIDE
-RSFA_DEFINE_KERNEL_LIST(kernels_wide, RSFA_WIDE_TILES(TypeF16, 0), RSFA_WIDE_TILES(TypeBF16, 1),
-                        RSFA_WIDE_TILES(TypeF16P8, 2))
+RSFA_DEFINE_KERNEL_LIST(kernels_wide, RSFA_WIDE_TILES(TypeF16, 0), RSFA_WIDE_TILES(TypeBF16, 1))
 #else
 namespace rsfa {
 KernelList kernels_wide() { return KernelList{nullptr, 0}; }

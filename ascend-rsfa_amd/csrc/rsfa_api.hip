@@ -444,8 +444,12 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     return RSFA_OK;
 }
 
+// Whether a float8 V is read as bytes by the kernels (head dim 128) rather
+// than from an fp16 copy.
+static bool v8_native(int64_t head_dim) { return head_dim == 128; }
+
 uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim) {
-    if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim)) return 0;
+    if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim) || v8_native(head_dim)) return 0;
     return (uint64_t)(z * h * n_ctx * head_dim) * 2;
 }
 
@@ -496,7 +500,8 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // launch could pick (before any device work): the K/V loader's per-lane
     // 32-bit offsets, and the split state's 32-bit rows (task * BLOCK_M + row
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
-    const int64_t v_rows = v8 ? a->head_dim : a->v_stride[2];  // a float8 V is read from its fp16 copy
+    // a float8 V is read from its fp16 copy, except at head dim 128 (bytes)
+    const int64_t v_rows = v8 && !v8_native(a->head_dim) ? a->head_dim : a->v_stride[2];
     for_each_kernel([&](const KernelEntry& e) {
         const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS
         if (st == RSFA_OK && e.dtype == a->dtype && e.d == a->head_dim &&
@@ -546,15 +551,16 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     p.neg = sc < 0.0f ? 1u : 0u;
 
     // workspace: the fp16 copy of a float8 V first, then the split state
-    const uint64_t v8_bytes = v8 ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
-    if (v8 || split) {
+    const bool v8_copy = v8 && !v8_native(a->head_dim);
+    const uint64_t v8_bytes = v8_copy ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
+    if (v8_copy || split) {
         const uint64_t need =
             v8_bytes + (split ? rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm) : 0);
         if (!ws || ws_bytes < need) return RSFA_E_WORKSPACE;
-        if (((uintptr_t)ws & (v8 ? 15 : 3)) != 0) return RSFA_E_ALIGN;
+        if (((uintptr_t)ws & (v8_copy ? 15 : 3)) != 0) return RSFA_E_ALIGN;
         if (split) p.state = (float*)((char*)ws + v8_bytes);
     }
-    if (v8) {
+    if (v8_copy) {
         uint32_t* wide = (uint32_t*)ws;
         const int lcpr = a->head_dim == 16 ? 0 : a->head_dim == 32 ? 1 : a->head_dim == 64 ? 2
                          : a->head_dim == 128 ? 3 : 4;  // log2 of the 16-byte chunks per row

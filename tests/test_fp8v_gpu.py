@@ -162,7 +162,8 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
 
 @pytest.mark.parametrize("N", [64, 1024])
 def test_pipelined_tile_within_the_rounding_bound(N):
-    """The float8 V path on the software-pipelined kernel (tile (256, 32))."""
+    """A (256, 32) tile request with a float8 V at head dim 128: the pipelined
+    kernel of that tile has no byte-V variant, so the nearest byte-V tile runs."""
     Z, H, D = 1, 4, 128
     q, k, v = A.make_inputs(Z, H, N, D, seed=N + 3)
     v8 = v.to(torch.float8_e5m2)
@@ -174,3 +175,36 @@ def test_pipelined_tile_within_the_rounding_bound(N):
     assert torch.isfinite(got).all()
     excess = ((got - exact).abs() - bound).max().item()
     assert excess <= 0, f"outside the bound by {excess}"
+
+
+@pytest.mark.parametrize("tile", [(256, 64), (256, 128), (128, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N,scale", [(1024, 0.1), (777, -0.3)])
+def test_byte_v_tiles_within_the_rounding_bound(tile, causal, N, scale):
+    """Head dim 128 reads a float8 V's bytes into LDS (no fp16 copy) and widens
+    each P.V operand in registers: every compiled tile (ping-pong (256, 64),
+    (256, 128), the 4-wave (128, 64)), whole and ragged key tiles, a negative
+    scale, more tasks than workgroups, against the exact result within the
+    per-element bound of the e5m2 rounding of P."""
+    Z, H, D = 2, 24, 128
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + tile[1] + int(causal))
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, causal, scale, BM=tile[0], BN=tile[1], exact_tile=True)
+    heads = [(0, 0), (0, 7), (1, 13), (Z - 1, H - 1)]
+    exact = A.reference_attention(q, k, v8.float(), causal, scale, heads=heads)
+    bound = A.fp8v_error_bound(q, k, v8, causal, scale, heads=heads)
+    got = torch.stack([o[z, h] for z, h in heads])
+    assert torch.isfinite(got).all()
+    excess = ((got - exact).abs() - bound).max().item()
+    assert excess <= 0, f"outside the bound by {excess}"
+
+
+def test_strided_byte_v_matches_contiguous():
+    """A float8 V read as bytes through its strides ([Z, N, H, D] storage)."""
+    q, k, v = A.make_inputs(2, 3, 700, 128, seed=31)
+    store = v.permute(0, 2, 1, 3).contiguous().to(torch.float8_e5m2)
+    v_view = store.permute(0, 2, 1, 3)
+    assert not v_view.is_contiguous()
+    a = _run(q, k, v_view.cuda(), True, 0.3)
+    b = _run(q, k, v_view.contiguous(), True, 0.3)
+    assert torch.equal(a, b)

@@ -146,13 +146,13 @@ def test_noalloc_under_graph_capture():
         assert not torch.isnan(oo.float()).any()
 
 
-def _cpu_args(**over):
+def _cpu_args(n=8192, d=128, **over):
     a = _native.FwdArgs()
     a.struct_size = ctypes.sizeof(a)
     a.dtype = _native.DTYPE_F16
     a.q = a.k = a.v = a.o = 0x1000
-    a.z, a.h, a.n_ctx, a.head_dim = 1, 8, 8192, 128
-    st = [8 * 8192 * 128, 8192 * 128, 128, 1]
+    a.z, a.h, a.n_ctx, a.head_dim = 1, 8, n, d
+    st = [8 * n * d, n * d, d, 1]
     for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
         getattr(a, name)[:] = st
     a.sm_scale, a.causal = 0.5, 0
@@ -164,11 +164,14 @@ def _cpu_args(**over):
 def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     lib = _native.lib()
     limit = _native.NOALLOC_WORKSPACE_BYTES
-    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x8192x128 is exactly the limit
-    fits = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2)
-    assert lib.rsfa_v8_workspace_bytes(1, 8, 8192, 128) == limit
-    over = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
+    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x16384x64 is exactly the limit
+    fits = _cpu_args(n=16384, d=64, dtype=_native.DTYPE_F16_V8E5M2)
+    assert lib.rsfa_v8_workspace_bytes(1, 8, 16384, 64) == limit
+    over = _cpu_args(n=16384, d=64, dtype=_native.DTYPE_F16_V8E5M2, z=2)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(over), None) == _native.E_SCRATCH
+    # at head dim 128 the kernels read a float8 V's bytes: no copy, any size
+    assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 128) == 0
+    big_v8 = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
     # split state: 8 bytes per query row, rounded to the tile
     split = _cpu_args(z=8, h=32, n_ctx=16384, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(split), None) == _native.E_SCRATCH
@@ -177,5 +180,5 @@ def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     assert lib.rsfa_attention_fwd_noalloc(None, None) == _native.E_NULL
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(_cpu_args(struct_size=8)), None) == _native.E_ABI
     if not torch.cuda.is_available():
-        for a in (fits, _cpu_args(z=8, h=32, n_ctx=16384, causal=1), _cpu_args(z=64)):
+        for a in (fits, big_v8, _cpu_args(z=8, h=32, n_ctx=16384, causal=1), _cpu_args(z=64)):
             assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(a), None) == _native.E_DEVICE
