@@ -39,6 +39,16 @@ sys.path.insert(0, ROOT)
 
 METRIC = "FA2 fwd TFLOP/s + % fp16 MFMA peak (causal & non-causal), ms/call"
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+PEAK_FP8_TFLOPS = 5000.0  # dense fp8 MFMA, published
+
+
+def peak_tflops(cfg):
+    """MFMA peak a config's work runs against: fp16, or for a float8 V (head
+    dim 128: P.V on the e5m2 MFMA) half the FLOPs (QK^T) at the fp16 rate and
+    half (P.V) at the fp8 rate, 1 / (0.5 / 2500 + 0.5 / 5000) = 3333 TFLOP/s."""
+    if len(cfg) > 8 and cfg[8] == "e5m2" and cfg[4] == 128:
+        return round(1.0 / (0.5 / PEAK_TFLOPS + 0.5 / PEAK_FP8_TFLOPS), 1)
+    return PEAK_TFLOPS
 PEAK_HBM_GBS = 8000.0
 
 # name, B, H, S, D, causal, sm_scale, seed[, V dtype]
@@ -149,7 +159,8 @@ def time_config(F, torch, cfg, steps, warmup, device_warmup_s=0.0, keep_cpu=Fals
     res = {
         "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "seed": seed, "tiling": [BM, BN],
         "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
-        "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / PEAK_TFLOPS, 2),
+        "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / peak_tflops(cfg), 2),
+        **({"peak_tflops": peak_tflops(cfg)} if peak_tflops(cfg) != PEAK_TFLOPS else {}),
         "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal, 1 if v8 else 2) / (ms * 1e-3) / 1e9, 1),
         "inputs_match_fingerprint": fp_ok,
         **({"v_dtype": "float8_e5m2"} if v8 else {}),
@@ -161,8 +172,9 @@ def roofline(cfg, res):
     """MFMA roofline of one config's kernel: algorithmic FLOPs per launch over
     the average launch duration of the timed region."""
     achieved = flops(*cfg[1:6]) / (res["ms_per_call"] * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": profile_traffic(cfg[0])}
+    peak = peak_tflops(cfg)
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": profile_traffic(cfg[0])}
 
 
 def calibrate_copy(torch, mib):
