@@ -1303,11 +1303,38 @@ fa_fwd_kernel(FwdParams p) {
                 int t = j0;
                 // one step: Y_t, then X_{t+1} (WQ: with the slots of the Q loads
                 // of the next task, from load qi on when qi >= 0)
-                auto pp_step = [&](auto wq, int qi, auto use_cb) {
+                // the loads of an X phase without its MFMAs (tl = t + 2)
+                auto x_loads = [&](int tl) {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+                    for (int q = 0; q < NSL; ++q)
+                        if (tl + 1 < jpp) pp_dma_at(kld, kgo, b_tv, q);
+#pragma unroll
+                    for (int q = 0; q < NSLV; ++q)
+                        if (tl < jpp) pp_dma_v_at(vld, b_t2 + TILE, q);
+                };
+                // DIAG_VM: steps that may reach the diagonal block (diag) mask
+                // the scores a wave's rows do not see.  A key tile wholly above
+                // this wave's rows has P = 0: from the first such tile on (but
+                // the last tile, whose masked softmax is harmless) the wave
+                // runs steps without its softmax, P.V and the next tile's S^T
+                // (above its rows too), keeping only the loads; when the four
+                // waves of a group skip, the phase lasts as long as the other
+                // group's work.
+                auto tile_hidden = [&](int tt) { return tt * BN > wq_hi; };
+                auto pp_advance = [&]() {
+                    kld += kstep;
+                    vld += vstep;
+                    const uint32_t b_old = b_tv;
+                    b_tv = b_t1;
+                    b_t1 = b_t2;
+                    b_t2 = b_old;
+                };
+                auto pp_step = [&](auto wq, int qi, auto use_cb, auto diag) {
                     phase_barrier();  // Y_t
                     prio_valu();
                     x8 pk[NKT][2];
-                    if constexpr (DIAG_VM) vmask(sacc, t);
+                    if constexpr (DIAG_VM && decltype(diag)::value) vmask(sacc, t);
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     if constexpr (DIAG_PP && decltype(use_cb)::value) {
@@ -1321,12 +1348,16 @@ fa_fwd_kernel(FwdParams p) {
                     phase_barrier();  // X_{t+1}
                     prio_mfma();
                     x_phase(std::integral_constant<int, NPV + NQK>(), t, t + 2, pk, sacc, wq, qi, use_cb);
-                    kld += kstep;
-                    vld += vstep;
-                    const uint32_t b_old = b_tv;
-                    b_tv = b_t1;
-                    b_t1 = b_t2;
-                    b_t2 = b_old;
+                    pp_advance();
+                };
+                // a step of a tile hidden from this wave: the barriers and loads only
+                auto pp_skip_step = [&]() {
+                    phase_barrier();  // Y_t
+                    prio_valu();
+                    phase_barrier();  // X_{t+1}
+                    prio_mfma();
+                    x_loads(t + 2);
+                    pp_advance();
                 };
                 if constexpr (QPF) {
                     // a task that loads the next task's Q (in X_{j0+2} and
@@ -1335,7 +1366,8 @@ fa_fwd_kernel(FwdParams p) {
                     // (a check in every MFMA phase cost more than the loads save)
                     if (qpf_do)
                         for (; t < j0 + 3; ++t)
-                            pp_step(std::true_type(), t == j0 ? -1 : (t - j0 - 1) * (NQD / 2), std::true_type());
+                            pp_step(std::true_type(), t == j0 ? -1 : (t - j0 - 1) * (NQD / 2), std::true_type(),
+                                    std::bool_constant<DIAG_VM>());  // (may reach the diagonal block: masked)
                 }
                 if constexpr (DIAG_PP) {
                     // steps whose key tile lies below the whole query block run
@@ -1343,11 +1375,23 @@ fa_fwd_kernel(FwdParams p) {
                     // the 32 bias VGPRs free the softmax phase is ~70 cycles
                     // shorter; the bias of the next tile is then filled whole
                     const int jd = m0 / BN;  // first key tile of the diagonal block
-                    for (; t + 1 < jpp && t + 1 < jd; ++t) pp_step(std::false_type(), -1, std::false_type());
+                    for (; t + 1 < jpp && t + 1 < jd; ++t) pp_step(std::false_type(), -1, std::false_type(), std::false_type());
 #pragma unroll
                     for (int kt = 0; kt < NKT; ++kt) cb_fill(kt, cb_rel(t + 1, kt));
                 }
-                for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1, std::true_type());
+                if constexpr (DIAG_VM) {
+                    // steps below the diagonal block need no mask and skip nothing
+                    // (separate loops: a skip branch inside the step made the
+                    // register allocator spill ~400 VGPRs; whether a tile is
+                    // hidden changes once per wave, so every wave still runs
+                    // the same steps and barriers)
+                    const int jd = m0 / BN;
+                    for (; t + 1 < jpp && t < jd; ++t) pp_step(std::false_type(), -1, std::true_type(), std::false_type());
+                    for (; t + 1 < jpp && !tile_hidden(t); ++t) pp_step(std::false_type(), -1, std::true_type(), std::true_type());
+                    for (; t + 1 < jpp; ++t) pp_skip_step();
+                } else {
+                    for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1, std::true_type(), std::false_type());
+                }
                 {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
