@@ -208,3 +208,21 @@ def test_strided_byte_v_matches_contiguous():
     a = _run(q, k, v_view.cuda(), True, 0.3)
     b = _run(q, k, v_view.contiguous(), True, 0.3)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("N", [1, 17, 100])
+@pytest.mark.parametrize("causal", [False, True])
+def test_byte_v_short_sequences(N, causal):
+    """Head dim 128 float8 V with fewer keys than one tile: the partial-tile
+    loads (rows past the sequence re-read its last row) and the masked P.V
+    (sub-tiles no row sees are not read) of the byte path."""
+    q, k, v = A.make_inputs(2, 3, N, 128, seed=40 + N)
+    v8 = v.to(torch.float8_e5m2)
+    o = _run(q, k, v8, causal, 0.2)
+    heads = [(0, 0), (1, 2)]
+    exact = A.reference_attention(q, k, v8.float(), causal, 0.2, heads=heads)
+    bound = A.fp8v_error_bound(q, k, v8, causal, 0.2, heads=heads)
+    got = torch.stack([o[z, h] for z, h in heads])
+    assert torch.isfinite(got).all()
+    excess = ((got - exact).abs() - bound).max().item()
+    assert excess <= 0, f"outside the bound by {excess}"
