@@ -430,14 +430,20 @@ fa_fwd_kernel(FwdParams p) {
     constexpr int TILE = BN * DP * 2;     // bytes of one K (or fp16 V) tile
     constexpr int NINST = BN * CPR / 64;  // 1-KB direct loads per tile
     // V8: V tiles of e5m2 bytes, BN rows of D bytes; the 1-KB slice s holds
-    // rows 8s..8s+7 whole, and row R keeps its 16-byte chunk c at position
-    // c ^ (R % 4 + 4 * ((R / 8) % 2)), so the eight rows one transposing read
-    // of P.V gathers (below) sit in eight different chunk columns.
+    // rows V8RPS*s.. whole, and row R keeps its 16-byte chunk c at column
+    // c ^ v8_swz(R), so the eight rows one transposing read of P.V gathers
+    // (below), and the sixteen (row, chunk) pairs of 32 lanes, fall in
+    // distinct banks: R % 4 + 4 ((R / 8) % 2) for 128-byte rows (rows 2 apart
+    // share banks), 2 ((R / 8) % 2) for 64-byte rows (rows 4 apart do).
     constexpr bool V8 = T::v8;
-    static_assert(!V8 || (D == 128 && BN % 64 == 0), "byte V tiles: head dim 128, 64-key groups");
+    static_assert(!V8 || ((D == 64 || D == 128) && BN % 64 == 0), "byte V tiles: head dim 64 or 128, 64-key groups");
     constexpr int TILEV = V8 ? BN * D : TILE;  // bytes of one V tile
     constexpr int BUF = TILE + TILEV;          // K + V
     constexpr int NINSTV = V8 ? TILEV / 1024 : NINST;
+    constexpr int V8RPS = 1024 / DP;           // rows per 1-KB slice of a byte V tile
+    constexpr int V8CPR = DP / 16;             // 16-byte chunks per row of it
+    // (rq = R % 4, rh = (R / 8) % 2 of the row)
+    auto v8_swz = [](int rq, int rh) { return D == 64 ? 2 * rh : rq + 4 * rh; };
     static_assert(BN % 32 == 0 && BN >= 32, "BN must be a multiple of 32");
     static_assert(D % 16 == 0, "D must be a multiple of 16");
     static_assert((BN * CPR) % 64 == 0, "tile must be whole 1-KB load slices");
@@ -530,11 +536,11 @@ fa_fwd_kernel(FwdParams p) {
     // Offset from the tile at q' = 0 (q' adds 16q' rows), per db.
     uint32_t vo8[V8 ? DT : 1];
     if constexpr (V8) {
-        const int tr = l16 >> 1;                                    // row r of the group
+        const int tr = l16 >> 1;  // row r of the group: R % 4 = r % 4, (R / 8) % 2 = r / 4
         const int rowb = D * (4 * hh + (tr & 3) + 8 * (tr >> 2)) + 8 * (l16 & 1);
-        const int x = ((lane >> 4) & 1) ^ tr;                       // chunk bit 0 ^ the row's swizzle
+        const int swz = v8_swz(tr & 3, tr >> 2);
 #pragma unroll
-        for (int db = 0; db < DT; ++db) vo8[db] = (uint32_t)(rowb + 16 * (x ^ (2 * db)));
+        for (int db = 0; db < DT; ++db) vo8[db] = (uint32_t)(rowb + 16 * ((2 * db + ((lane >> 4) & 1)) ^ swz));
     }
 
     // Loader: in every 1-KB slice lane i fills chunk 4*cg + i/16 of the 16-row
@@ -556,13 +562,17 @@ fa_fwd_kernel(FwdParams p) {
         if constexpr (!V8) vgo[sl] = (uint32_t)(((16 * blk + ld_rib) * p.v_sn + cg * 32 + ld_chl * 8) * 2);
     }
     // V8: lane i of slice s fills position i of the slice, i.e. chunk column
-    // i % 8 of row 8s + i / 8, with the row's chunk (i % 8) ^ swizzle
-    auto v8_chunk = [&](int s) { return (lane & 7) ^ ((lane >> 3) & 3) ^ (4 * (s & 1)); };
+    // i % V8CPR of row V8RPS*s + i / V8CPR, with that row's chunk
+    // (i % V8CPR) ^ v8_swz(row)
+    auto v8_chunk = [&](int s) {
+        const int row = V8RPS * s + lane / V8CPR;
+        return (lane % V8CPR) ^ v8_swz(row & 3, (row >> 3) & 1);
+    };
     if constexpr (V8) {
 #pragma unroll
         for (int sl = 0; sl < NSLV; ++sl) {
             const int s = sl * NW + wave;
-            vgo[sl] = (uint32_t)((8 * s + (lane >> 3)) * p.v_sn + 16 * v8_chunk(s));
+            vgo[sl] = (uint32_t)((V8RPS * s + lane / V8CPR) * p.v_sn + 16 * v8_chunk(s));
         }
     }
     // Q rows (QPF): each wave loads its own 32 rows, i.e. the slices of the two
@@ -665,8 +675,8 @@ fa_fwd_kernel(FwdParams p) {
                 for (int sl = 0; sl < NSLV; ++sl) {
                     const int s = sl * NW + wave;
                     if (NINSTV % NW == 0 || s < NINSTV) {
-                        const int row0 = min(8 * s, last);
-                        const int rr = min(8 * s + (lane >> 3), last) - row0;
+                        const int row0 = min(V8RPS * s, last);
+                        const int rr = min(V8RPS * s + lane / V8CPR, last) - row0;
                         const uint32_t vo = (uint32_t)(rr * p.v_sn + 16 * v8_chunk(s));
                         dma16(vt0 + (int64_t)row0 * p.v_sn, vo, dst0 + TILE + s * 1024);
                     }

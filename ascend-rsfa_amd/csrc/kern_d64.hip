@@ -9,5 +9,6 @@ using namespace rsfa;
 #define RSFA_D64_TILES(T, DTYPE) RSFA_TILE_ENTRIES(T, DTYPE, 64, 128, 8, 2), RSFA_TILE_ENTRIES(T, DTYPE, 64, 64, 4, 2)
 #endif
 
+// float8 V: V's bytes go into LDS as they are (TypeF16V8)
 RSFA_DEFINE_KERNEL_LIST(kernels_d64, RSFA_D64_TILES(TypeF16, 0), RSFA_D64_TILES(TypeBF16, 1),
-                        RSFA_D64_TILES(TypeF16P8, 2))
+                        RSFA_D64_TILES(TypeF16V8, 2))

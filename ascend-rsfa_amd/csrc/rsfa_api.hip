@@ -444,9 +444,9 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     return RSFA_OK;
 }
 
-// Whether a float8 V is read as bytes by the kernels (head dim 128) rather
-// than from an fp16 copy.
-static bool v8_native(int64_t head_dim) { return head_dim == 128; }
+// Whether a float8 V is read as bytes by the kernels (head dims 64 and 128)
+// rather than from an fp16 copy.
+static bool v8_native(int64_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
 uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim) {
     if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim) || v8_native(head_dim)) return 0;

@@ -136,9 +136,11 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
     from ascend_rsfa import _native
 
     lib = _native.lib()
-    q, k, v = (t.cuda() for t in A.make_inputs(1, 2, 128, 64, seed=23))
+    # head dim 32: a float8 V goes through its fp16 copy (64 and 128 read the bytes)
+    q, k, v = (t.cuda() for t in A.make_inputs(1, 2, 128, 32, seed=23))
     v8, o = v.to(torch.float8_e5m2), torch.empty_like(q)
-    need = int(lib.rsfa_v8_workspace_bytes(1, 2, 128, 64))
+    need = int(lib.rsfa_v8_workspace_bytes(1, 2, 128, 32))
+    assert need > 0 and lib.rsfa_v8_workspace_bytes(1, 2, 128, 64) == 0
     ws = torch.empty(need // 4 + 16, dtype=torch.float32, device="cuda")
     run = lambda a: lib.rsfa_attention_fwd(ctypes.byref(a), None)  # noqa: E731
     print("workspace checks", flush=True)
@@ -148,7 +150,7 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
     assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, ws=ws.data_ptr() + 4, ws_bytes=need)) == \
         _native.E_ALIGN
     # causal split: the state after the float8 V copy, both counted
-    split = int(lib.rsfa_split_workspace_bytes(1, 2, 128, 64, 128))
+    split = int(lib.rsfa_split_workspace_bytes(1, 2, 128, 32, 128))
     assert run(_raw_args(q, k, q, o, 0, causal=True, flags=_native.FLAG_CAUSAL_SPLIT)) == _native.E_WORKSPACE
     big = torch.empty((need + split) // 4 + 16, dtype=torch.float32, device="cuda")
     a = _raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, causal=True, flags=_native.FLAG_CAUSAL_SPLIT,
@@ -177,17 +179,19 @@ def test_pipelined_tile_within_the_rounding_bound(N):
     assert excess <= 0, f"outside the bound by {excess}"
 
 
-@pytest.mark.parametrize("tile", [(256, 64), (256, 128), (128, 64)])
+@pytest.mark.parametrize("D,tile", [(128, (256, 64)), (128, (256, 128)), (128, (128, 64)),
+                                    (64, (256, 128)), (64, (128, 64))])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("N,scale", [(1024, 0.1), (777, -0.3)])
-def test_byte_v_tiles_within_the_rounding_bound(tile, causal, N, scale):
-    """Head dim 128 reads a float8 V's bytes into LDS (no fp16 copy) and widens
-    each P.V operand in registers: every compiled tile (ping-pong (256, 64),
-    (256, 128), the 4-wave (128, 64)), whole and ragged key tiles, a negative
-    scale, more tasks than workgroups, against the exact result within the
-    per-element bound of the e5m2 rounding of P."""
-    Z, H, D = 2, 24, 128
-    q, k, v = A.make_inputs(Z, H, N, D, seed=N + tile[1] + int(causal))
+def test_byte_v_tiles_within_the_rounding_bound(D, tile, causal, N, scale):
+    """Head dims 64 and 128 read a float8 V's bytes into LDS (no fp16 copy)
+    and run P.V on the e5m2 MFMA: every compiled tile (D=128: ping-pong
+    (256, 64), (256, 128), the 4-wave (128, 64); D=64: ping-pong (256, 128),
+    4-wave (128, 64)), whole and ragged key tiles, a negative scale, more tasks
+    than workgroups, against the exact result within the per-element bound of
+    the e5m2 rounding of P."""
+    Z, H = 2, 24
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + tile[1] + int(causal) + D)
     v8 = v.to(torch.float8_e5m2)
     o = _run(q, k, v8, causal, scale, BM=tile[0], BN=tile[1], exact_tile=True)
     heads = [(0, 0), (0, 7), (1, 13), (Z - 1, H - 1)]

@@ -164,12 +164,12 @@ def _cpu_args(n=8192, d=128, **over):
 def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     lib = _native.lib()
     limit = _native.NOALLOC_WORKSPACE_BYTES
-    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x16384x64 is exactly the limit
-    fits = _cpu_args(n=16384, d=64, dtype=_native.DTYPE_F16_V8E5M2)
-    assert lib.rsfa_v8_workspace_bytes(1, 8, 16384, 64) == limit
-    over = _cpu_args(n=16384, d=64, dtype=_native.DTYPE_F16_V8E5M2, z=2)
+    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x4096x256 is exactly the limit
+    fits = _cpu_args(n=4096, d=256, dtype=_native.DTYPE_F16_V8E5M2)
+    assert lib.rsfa_v8_workspace_bytes(1, 8, 4096, 256) == limit
+    over = _cpu_args(n=4096, d=256, dtype=_native.DTYPE_F16_V8E5M2, z=2)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(over), None) == _native.E_SCRATCH
-    # at head dim 128 the kernels read a float8 V's bytes: no copy, any size
+    # at head dims 64 and 128 the kernels read a float8 V's bytes: no copy, any size
     assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 128) == 0
     big_v8 = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
     # split state: 8 bytes per query row, rounded to the tile
