@@ -1399,6 +1399,10 @@ fa_fwd_kernel(FwdParams p) {
                     for (; t + 1 < jpp && t < jd; ++t) pp_step(std::false_type(), -1, std::true_type(), std::false_type());
                     for (; t + 1 < jpp && !tile_hidden(t); ++t) pp_step(std::false_type(), -1, std::true_type(), std::true_type());
                     for (; t + 1 < jpp; ++t) pp_skip_step();
+                } else if constexpr (DIAG_PP) {
+                    // the same skip of hidden diagonal tiles (bias blocks mask the others)
+                    for (; t + 1 < jpp && !tile_hidden(t); ++t) pp_step(std::false_type(), -1, std::true_type(), std::false_type());
+                    for (; t + 1 < jpp; ++t) pp_skip_step();
                 } else {
                     for (; t + 1 < jpp; ++t) pp_step(std::false_type(), -1, std::true_type(), std::false_type());
                 }
@@ -1407,6 +1411,15 @@ fa_fwd_kernel(FwdParams p) {
                     prio_valu();
                     x8 pk[NKT][2];
                     if constexpr (DIAG_VM) vmask(sacc, t);
+                    if constexpr (DIAG_PP) {
+                        // a last tile hidden from this wave: its S^T was not
+                        // formed (skipped steps), and its P must be 0
+                        const bool hid = tile_hidden(t);
+#pragma unroll
+                        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) sacc[kt][i] = hid ? -INFINITY : sacc[kt][i];
+                    }
                     softmax_part(sacc, pk, mask_free);
                     if constexpr (LSUM_IN_Y) asm volatile("" : "+v"(l_sum));
                     phase_barrier();  // its PV
