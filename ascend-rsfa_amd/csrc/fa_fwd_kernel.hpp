@@ -318,17 +318,6 @@ __device__ __forceinline__ i32x2 lds_read_tr8(uint32_t addr) {
     return r;
 }
 
-// Eight e5m2 bytes (byte e = element e) as eight fp16: the fp16 with the value
-// of an e5m2 byte b has the bits b << 8 (same sign, exponent bias and width,
-// two more mantissa bits), so the widening is exact.
-// One v_perm_b32 per two elements: selector byte k picks byte k of the 64-bit
-// {0, w} (0-3: w) or, as 0x0C, a zero byte.
-__device__ __forceinline__ i32x4 widen_e5m2x8(i32x2 r) {
-    const uint32_t lo = (uint32_t)r[0], hi = (uint32_t)r[1];
-    return (i32x4){(int)__builtin_amdgcn_perm(0u, lo, 0x010C000Cu), (int)__builtin_amdgcn_perm(0u, lo, 0x030C020Cu),
-                   (int)__builtin_amdgcn_perm(0u, hi, 0x010C000Cu), (int)__builtin_amdgcn_perm(0u, hi, 0x030C020Cu)};
-}
-
 // The float8 P.V MFMA's operands: A from four byte-transposing reads (8
 // bytes each), B from the P bytes of two 32-key sub-tiles (16 each).
 __device__ __forceinline__ i32x8 cat4(i32x2 r0, i32x2 r1, i32x2 r2, i32x2 r3) {
@@ -527,13 +516,14 @@ fa_fwd_kernel(FwdParams p) {
         voff[u] = vcc * 256 + (((8 * u + 4 * hh + (l16 >> 2)) ^ (4 * vcc)) * 16) + 8 * (l16 & 1);
     // V8 (ds_read_b64_tr_b8): in a 16-lane group lanes 2r and 2r+1 address
     // bytes 0-7 and 8-15 of row r of eight rows, and the hardware hands lane j
-    // column j of the eight rows.  For the P.V MFMA of 16-key group q' (keys
-    // 16q'.. of the tile) and head-dim block db, operand byte e of lane
-    // (d + 32 hh) must be key 16q' + 4hh + e % 4 + 8 (e / 4), the key whose
-    // rounded P that lane holds in byte slot e of its P^T operand (the S^T
-    // accumulator layout); so row r of the group is that key for e = r, and
-    // the group's 16 columns are head dims 32db + 16((lane / 16) % 2) ...
-    // Offset from the tile at q' = 0 (q' adds 16q' rows), per db.
+    // column j of the eight rows.  The read of 16-key group q' (keys 16q'.. of
+    // the tile) and head-dim block db gives bytes 8 (q' % 4) .. +7 of the A
+    // operand (V^T) of the 64-key float8 MFMA of keys 64 (q' / 4).. ; its byte
+    // e must be key 16q' + 4hh + e % 4 + 8 (e / 4) for lane (d + 32 hh), the
+    // key whose rounded P that lane holds in the same byte of its B operand
+    // (P^T, in the S^T accumulator layout); so row r of the group is that key
+    // for e = r, and the group's 16 columns are head dims 32db + 16((lane /
+    // 16) % 2) ...  Offset from the tile at q' = 0 (q' adds 16q' rows), per db.
     uint32_t vo8[V8 ? DT : 1];
     if constexpr (V8) {
         const int tr = l16 >> 1;  // row r of the group: R % 4 = r % 4, (R / 8) % 2 = r / 4
