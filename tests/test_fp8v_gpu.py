@@ -90,8 +90,12 @@ def test_strided_float8_v_matches_contiguous():
     assert torch.equal(a, b)
 
 
-def test_split_mode_with_float8_v():
-    q, k, v = A.make_inputs(1, 4, 700, 128, seed=17)
+@pytest.mark.parametrize("D", [64, 128, 32])
+def test_split_mode_with_float8_v(D):
+    """The two-launch causal split with a float8 V: the byte path (D = 64,
+    128) and the fp16 copy (D = 32), the copy then the split state in one
+    workspace."""
+    q, k, v = A.make_inputs(1, 4, 700, D, seed=17)
     v8 = v.to(torch.float8_e5m2)
     o = _run(q, k, v8, True, 0.25, split=True)
     heads = [(0, 0), (0, 3)]
