@@ -234,3 +234,21 @@ def test_byte_v_short_sequences(N, causal):
     assert torch.isfinite(got).all()
     excess = ((got - exact).abs() - bound).max().item()
     assert excess <= 0, f"outside the bound by {excess}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_float8_v_lse_is_the_exact_logsumexp(D, causal):
+    """With a float8 V the row sums add the unrounded P (as the reference's
+    fp8_v branch), so the LSE output is the logsumexp of the scaled scores,
+    independent of V's rounding: the oracle's exact LSE to 1e-3."""
+    q, k, v = A.make_inputs(2, 3, 333, D, seed=50 + D)
+    v8 = v.to(torch.float8_e5m2)
+    print(f"fp8v lse: D={D} causal={causal}", flush=True)
+    o, lse = faf.forward(q.cuda(), k.cuda(), v8.cuda(), causal, 0.3, return_lse=True)
+    torch.cuda.synchronize()
+    heads = [(0, 1), (1, 2)]
+    _, ref_lse = A.reference_attention(q, k, v.float(), causal, 0.3, return_lse=True, heads=heads)
+    got = torch.stack([lse[z, h].cpu() for z, h in heads])
+    assert torch.isfinite(got).all()
+    assert (got - ref_lse).abs().max().item() < 1e-3
