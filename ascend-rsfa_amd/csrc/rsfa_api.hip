@@ -500,7 +500,8 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // launch could pick (before any device work): the K/V loader's per-lane
     // 32-bit offsets, and the split state's 32-bit rows (task * BLOCK_M + row
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
-    // a float8 V is read from its fp16 copy, except at head dim 128 (bytes)
+    // a float8 V is read from its fp16 copy, except at head dims 64 and 128
+    // (bytes, whose offsets are half those of the fp16 check)
     const int64_t v_rows = v8 && !v8_native(a->head_dim) ? a->head_dim : a->v_stride[2];
     for_each_kernel([&](const KernelEntry& e) {
         const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS
