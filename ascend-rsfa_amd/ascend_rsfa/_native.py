@@ -9,7 +9,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "librsfa.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # rsfa_status
 OK = 0
@@ -34,6 +34,7 @@ DTYPE_F16_V8E5M2 = 2  # q, k, o float16; v float8_e5m2
 FLAG_STATIC_SCHEDULE = 0x1
 FLAG_CAUSAL_SPLIT = 0x2
 FLAG_EXACT_TILE = 0x4
+FLAG_TILE_HINT = 0x8
 
 # rsfa_attention_fwd_noalloc's fixed workspace
 NOALLOC_WORKSPACE_BYTES = 16 << 20

@@ -24,17 +24,24 @@ that are not on a GPU, the calls raise.
 
 A ``float8_e5m2`` V with float16 Q and K runs the reference's fp8_v branch
 (_attn_fwd_inner 208-211, 217): P is rounded to e5m2 for P.V while the row
-sums add the unrounded P; O is float16.  The library widens V to fp16 in a
-workspace first (exact: an e5m2 byte is the high byte of that fp16).
+sums add the unrounded P; O is float16.  At head dims 64 and 128 the kernels
+read V's bytes and run P.V on the e5m2 MFMA; at head dims 16, 32 and 256 the
+library first widens V to fp16 in a workspace (exact: an e5m2 byte is the
+high byte of that fp16) and P is rounded to e5m2 and widened back.
+
+``BM``/``BN`` keep the reference's meaning (query rows per program, keys per
+inner tile) and its validity rules: they select the tile, and the compiled
+gfx950 tile nearest to the request runs (``resolve_tiling``), so a harness
+that times ``attention`` per (BM, BN) candidate, as the reference's tiling
+search does, times distinct kernels.  ``BM = BN = 0`` runs ``get_tiling``'s
+tile.  Hint mode (``forward(..., tile_hint=True)``, or the environment
+variable ``RSFA_TILE_HINT=1`` for every call, ``attention`` included) only
+checks a request and runs ``get_tiling``'s tile for the shape, for callers
+whose tiles were tuned for Ascend's unified buffer.
 
 Behaviour beyond the reference (documented, deliberate):
 
-* ``BM``/``BN`` keep the reference's meaning (query rows per program, keys per
-  inner tile) and its validity rules, and are a tuning hint as they are in the
-  reference: the tile ``get_tiling`` picks for the shape runs, since values
-  tuned for Ascend's unified buffer say nothing about gfx950
-  (``forward(..., exact_tile=True)`` runs the nearest compiled tile instead).
-  Causal calls with ``BN > BM``, which give NaN in the reference
+* Causal calls with ``BN > BM``, which give NaN in the reference
   (benchmarks/run_correctness_test.py:24-25), raise ``ValueError`` instead.
 * Any ``N_CTX >= 1`` works (the reference has no load masks, so it needs
   ``N_CTX`` divisible by its tiles).
@@ -110,8 +117,8 @@ def get_tiling(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16):
     ``RSFA_TILING_CACHE``; entries that are not a compiled tile shape are
     ignored); otherwise the library searches the compiled gfx950 tile shapes
     with an LDS feasibility check and a makespan model of the persistent grid
-    on the current device's CUs, so it answers for every valid shape.  This is
-    the tile ``attention`` runs.
+    on the current device's CUs, so it answers for every valid shape.
+    ``attention`` called with this tile (or with ``BM = BN = 0``) runs it.
     """
     cache = _package_module("tiling").active_cache()
     if cache is not None:
@@ -144,8 +151,8 @@ def resolve_tiling(HEAD_DIM, causal, BM, BN, dtype=torch.float16):
     """The compiled (BLOCK_M, BLOCK_N) instantiation nearest to a request.
 
     Raises ValueError for a request the reference's rules reject.  This is the
-    tile ``forward(..., exact_tile=True)`` runs; without ``exact_tile`` a valid
-    request is a hint and the tile of ``get_tiling`` runs.
+    tile ``attention`` / ``forward`` run for the request (in hint mode the
+    tile of ``get_tiling`` runs instead).
     """
     bm = ctypes.c_int32()
     bn = ctypes.c_int32()
@@ -156,6 +163,8 @@ def resolve_tiling(HEAD_DIM, causal, BM, BN, dtype=torch.float16):
 
 
 def split_workspace_bytes(Z, H, N_CTX, HEAD_DIM, BM):
+    """Workspace of split mode for the BLOCK_M that runs: fp32 (m, l) and the
+    un-normalised fp32 accumulator of every query row of every task."""
     return int(_native.lib().rsfa_split_workspace_bytes(int(Z), int(H), int(N_CTX), int(HEAD_DIM), int(BM)))
 
 
@@ -175,16 +184,26 @@ def _as_kernel_layout(t):
     return t
 
 
+def _hint_mode(tile_hint, exact_tile):
+    if exact_tile:
+        return False
+    if tile_hint is not None:
+        return bool(tile_hint)
+    return os.environ.get("RSFA_TILE_HINT", "").strip().lower() in ("1", "true", "yes", "on")
+
+
 def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=False,
-            static_schedule=False, exact_tile=False, out=None):
+            static_schedule=False, tile_hint=None, exact_tile=False, out=None):
     """Run the forward kernel; returns ``o`` or ``(o, lse)``.
 
     ``BM``/``BN`` keep the reference's meaning and validity rules (ValueError
-    otherwise) but are a hint: the tile ``get_tiling`` picks for the shape
-    runs, as the reference's values are tuned for Ascend.  ``exact_tile=True``
-    runs the compiled tile nearest to the request instead (``resolve_tiling``);
-    ``BM = BN = 0`` is no request.  ``split=True`` (causal only) runs the
-    reference's two-launch prefix/diagonal split with an fp32 state workspace;
+    otherwise) and select the tile: the compiled tile nearest to the request
+    runs (``resolve_tiling``); ``BM = BN = 0`` runs ``get_tiling``'s tile.
+    ``tile_hint=True`` (default: the ``RSFA_TILE_HINT`` environment variable)
+    only checks a request and runs ``get_tiling``'s tile; ``exact_tile=True``
+    overrides hint mode.  ``split=True`` (causal only) runs the reference's
+    two-launch prefix/diagonal split, handing (m, l, acc) over in an fp32
+    workspace;
     ``static_schedule=True`` replaces the dynamic task queue by the
     reference's grid-stride order (results are bitwise identical).  ``lse`` is
     the natural-log logsumexp of the scaled scores, fp32 [Z, H, N].
@@ -226,7 +245,7 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
         # The tile is settled here and passed as an exact request, so the
         # launch runs the same tile the split workspace is sized for, and a
         # get_tiling answer from a measured cache is honoured.
-        if (BM or BN) and exact_tile:
+        if (BM or BN) and not _hint_mode(tile_hint, exact_tile):
             bm, bn = resolve_tiling(D, causal, BM, BN, q.dtype)
         else:
             if BM or BN:

@@ -175,7 +175,7 @@ def search_case(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16, sm_scale=0.5
         from .flash_attention_forward import forward
 
         def attention_fn(q, k, v, causal, sm_scale, bm, bn):
-            # each candidate runs its own instantiation (a plain request is a hint)
+            # each candidate runs its own instantiation, whatever RSFA_TILE_HINT says
             return forward(q, k, v, causal, sm_scale, bm, bn, exact_tile=True)
     if device is None:
         device = torch.device("cuda", torch.cuda.current_device())
@@ -238,11 +238,11 @@ def compare_reference_tilings(warmup=2, iters=5, sm_scale=0.5, rounds=6, verbose
     """The reference's 12 cases timed three ways on this GPU.
 
     * ``ours``: ``attention(..., *get_tiling(...))``, this build's choice;
-    * ``ref_hint``: ``attention(..., BM, BN)`` with the reference's tile for
-      the case, the call a reference user makes (the request is a hint, so it
-      runs the tile of ``get_tiling`` as well);
-    * ``ref_exact``: ``forward(..., BM, BN, exact_tile=True)``, the compiled
-      tile nearest to the reference's request forced.
+    * ``ref_hint``: ``forward(..., BM, BN, tile_hint=True)`` with the
+      reference's tile for the case: the request is only checked and the tile
+      of ``get_tiling`` runs (hint mode, ``RSFA_TILE_HINT=1``);
+    * ``ref_exact``: ``attention(..., BM, BN)``, the call a reference user
+      makes: the compiled tile nearest to the reference's request.
 
     Inputs: Q, K, V ~ N(0, 0.5^2) in fp16 drawn on the GPU (seed 7 + case),
     sm_scale 0.5, as the reference's benchmark harness uses
@@ -263,7 +263,7 @@ def compare_reference_tilings(warmup=2, iters=5, sm_scale=0.5, rounds=6, verbose
         exact = tuple(resolve_tiling(D, causal, *ref_tile, dtype=dtype))
         runs = {
             "ours": lambda: attention(q, k, v, causal, sm_scale, *ours),
-            "ref_hint": lambda: attention(q, k, v, causal, sm_scale, *ref_tile),
+            "ref_hint": lambda: forward(q, k, v, causal, sm_scale, *ref_tile, tile_hint=True),
             "ref_exact": lambda: forward(q, k, v, causal, sm_scale, *ref_tile, exact_tile=True),
         }
         fl = 4.0 * Z * H * N * N * D * (0.5 if causal else 1.0)

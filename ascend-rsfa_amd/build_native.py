@@ -39,10 +39,8 @@ HIPCC_FLAGS = [
     "-I" + os.path.join(REPO_ROOT, "include"),
 ]
 
-# Per-file flags.  kern_wide.hip: MFMAs in the VGPR form (accumulators in
-# VGPRs) for the one-wave-per-SIMD kernel; the compiler then places values
-# only MFMAs read (the Q^T operands) in AGPRs.
-FILE_FLAGS = {"kern_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Per-file flags (none at present; kept for instantiation units that need their own).
+FILE_FLAGS = {}
 
 
 def hipcc():

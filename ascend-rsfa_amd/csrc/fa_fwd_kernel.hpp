@@ -159,6 +159,7 @@ struct FwdParams {
     void* o;
     float* lse;      // optional [Z*H, n_ctx]
     float* state;    // split mode: [2][Z*H*nmb*BM] (m, l) per query row
+    float* acc;      // split mode: [Z*H*nmb*BM][D] un-normalised fp32 accumulator per query row
     int64_t q_sz, q_sh, q_sm;
     int64_t k_sz, k_sh, k_sn;
     int64_t v_sz, v_sh, v_sn;
@@ -856,25 +857,27 @@ fa_fwd_kernel(FwdParams p) {
         };
 
         const int srow = bh * p.nmb * BM + m0 + wave * 32 + l32;  // split-state row
+        // split mode: this row's fp32 accumulator in the workspace (every
+        // row of every task has one, rows past n included)
+        float* const acc_row = MODE == MODE_FUSED ? nullptr : p.acc + (int64_t)srow * D;
         if (MODE == MODE_DIAG) {
-            // resume from the prefix launch: O holds acc/l in the input dtype
-            const float sm = p.state[srow];
-            const float sl = p.state[(int64_t)p.num_tasks * BM + srow];
-            m_use = sm;
-            l_sum = hh == 0 ? sl : 0.0f;
-            if (qrow < n) {
+            // resume from the prefix launch: its (m, l) and un-normalised
+            // accumulator, all fp32
+            m_use = p.state[srow];
+            l_sum = hh == 0 ? p.state[(int64_t)p.num_tasks * BM + srow] : 0.0f;
 #pragma unroll
-                for (int d = 0; d < DT; ++d)
+            for (int d = 0; d < DT; ++d)
 #pragma unroll
-                    for (int a = 0; a < 4; ++a) {
-                        const int col = 32 * d + 8 * a + 4 * hh;
-                        if (col < D) {
-                            const x4 v4 = *(const x4*)(ob + (int64_t)qrow * p.o_sm + col);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) o[d][4 * a + e] = (float)v4[e] * sl;
-                        }
+                for (int a = 0; a < 4; ++a) {
+                    const int col = 32 * d + 8 * a + 4 * hh;
+                    if (col < D) {
+                        const float4 v4 = *(const float4*)(acc_row + col);
+                        o[d][4 * a + 0] = v4.x;
+                        o[d][4 * a + 1] = v4.y;
+                        o[d][4 * a + 2] = v4.z;
+                        o[d][4 * a + 3] = v4.w;
                     }
-            }
+                }
         }
 
         const int wq_lo = m0 + wave * 32;  // smallest query row of this wave
@@ -1453,13 +1456,7 @@ fa_fwd_kernel(FwdParams p) {
         // publishes them)
         if constexpr (QPF) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const float lt = swap_sum(l_sum);
-        if (MODE == MODE_PREFIX) {
-            if (hh == 0) {
-                p.state[srow] = m_use;
-                p.state[(int64_t)p.num_tasks * BM + srow] = lt;
-            }
-        }
-        const float inv = (MODE == MODE_PREFIX) ? (lt > 0.0f ? 1.0f / lt : 0.0f) : 1.0f / lt;
+        const float inv = 1.0f / lt;
         // O leaves through LDS: in the accumulator layout a lane holds 8 bytes
         // of a row per (d, a), so a direct store instruction writes 32 rows x
         // 16 bytes, and a CU needs ~64 cycles per such instruction (measured:
@@ -1473,7 +1470,24 @@ fa_fwd_kernel(FwdParams p) {
                               : NW * 32 * (D + 16) <= NBUF * BUF ? D / 2 : D / 4;
         constexpr int OROW = 2 * OCOLS + 16;  // bytes per staged row (16-byte pad)
         constexpr bool OSTAGE = NW * 32 * OROW <= NBUF * BUF && OCOLS >= 16;
-        if constexpr (OSTAGE) {
+        if constexpr (MODE == MODE_PREFIX) {
+            // hand (m, l) and the un-normalised accumulator to the diagonal
+            // launch in fp32 (the reference rounds acc to the input dtype
+            // into O, 353)
+            if (hh == 0) {
+                p.state[srow] = m_use;
+                p.state[(int64_t)p.num_tasks * BM + srow] = lt;
+            }
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) {
+                    const int col = 32 * d + 8 * a + 4 * hh;
+                    if (col < D)
+                        *(float4*)(acc_row + col) =
+                            make_float4(o[d][4 * a + 0], o[d][4 * a + 1], o[d][4 * a + 2], o[d][4 * a + 3]);
+                }
+        } else if constexpr (OSTAGE) {
             __syncthreads();  // every wave is done with the K/V tiles
             // a wave's own region: its reads of one round precede (in LDS
             // order) its writes of the next, so rounds need no barrier
@@ -1503,7 +1517,7 @@ fa_fwd_kernel(FwdParams p) {
                     if (row0 + r < n) *(x8*)(ob + (int64_t)(row0 + r) * p.o_sm + hf * OCOLS + cc) = v;
                 }
             }
-            if (MODE != MODE_PREFIX && p.lse && hh == 0 && qrow < n)
+            if (p.lse && hh == 0 && qrow < n)
                 p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;
         } else if (qrow < n) {
 #pragma unroll
@@ -1518,7 +1532,7 @@ fa_fwd_kernel(FwdParams p) {
                         *(x4*)(ob + (int64_t)qrow * p.o_sm + col) = v4;
                     }
                 }
-            if (MODE != MODE_PREFIX && p.lse && hh == 0)
+            if (p.lse && hh == 0)
                 p.lse[(int64_t)bh * n + qrow] = (m_use + __log2f(lt)) * 0.69314718055994530942f;
         }
 

@@ -40,8 +40,7 @@ static_assert(kSlotWords * sizeof(uint32_t) <= kScratchCounterBytes, "the counte
 constexpr int kLdsPerCu = 160 * 1024;   // gfx950
 constexpr int kMaxKernels = 512;        // instantiations in all kernel lists
 
-KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256(),
-                          kernels_wide()};
+KernelList all_lists[] = {kernels_d16(), kernels_d32(), kernels_d64(), kernels_d128(), kernels_d256()};
 
 template <class F>
 void for_each_kernel(F&& f) {
@@ -57,10 +56,6 @@ const KernelEntry* find_kernel(int dtype, int d, int bn, int bm, int causal, int
     });
     return hit;
 }
-
-// Whether an instantiation can run a sequence of n_ctx keys: the
-// one-wave-per-SIMD kernel needs whole key tiles.
-bool runs_shape(const KernelEntry& e, int64_t n_ctx) { return !e.wide || n_ctx % e.bn == 0; }
 
 bool valid_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -206,14 +201,6 @@ struct TileCost {
 // other wave's MFMAs.
 double wave_tile_cycles(const KernelEntry& e) {
     const int dp = e.d < 32 ? 32 : e.d;
-    if (e.wide) {
-        // 32 * wide rows per wave: both contractions on MFMA with the softmax
-        // interleaved into them, one barrier per pair of tiles.  Measured on
-        // MI355X (B=128 H=8 S=2048 D=128): 1024 TFLOP/s for 32 rows per wave,
-        // 1002 for 64, against 1103 for the ping-pong (256, 64) tile.
-        const double mfma = 2.0 * 2.0 * 32.0 * e.wide * e.bn * dp / 1024.0;
-        return mfma * (e.wide == 1 ? 1.53 : 1.57) + 60.0;
-    }
     const double mfma = 2.0 * 2.0 * 32.0 * e.bn * dp / 1024.0;
     const double valu = (9.5 * e.bn / 2.0 + 300.0 * e.bn / 64.0) * (e.pp ? 0.75 : 1.0);
     const double sync = e.nw >= 8 ? 100.0 : 300.0;
@@ -225,8 +212,8 @@ TileCost tile_cost(const KernelEntry& e, int64_t z, int64_t h, int64_t n, int nu
     const int dp = e.d < 32 ? 32 : e.d;
     // Each instantiation was compiled for `occ` waves per SIMD (the compiler
     // fits its registers to that), so only the LDS budget is checked here.
-    const int lds = (e.wide ? e.nbuf : e.pp ? 3 : 2) * 2 * e.bn * dp * 2;
-    if (lds > kLdsPerCu || !runs_shape(e, n)) return tc;
+    const int lds = (e.pp ? 3 : 2) * 2 * e.bn * dp * 2;
+    if (lds > kLdsPerCu) return tc;
     const int wg_by_waves = (4 * e.occ) / e.nw;
     const int wg_by_lds = kLdsPerCu / lds;
     const int wg_per_cu = std::max(1, std::min(wg_by_waves, wg_by_lds));
@@ -289,16 +276,14 @@ int validate_request(int causal, int req_bm, int req_bn) {
 }
 
 // The compiled instantiation nearest to a valid request (log distance in BM
-// and BN; ties go to the larger BN).  This is what RSFA_FLAG_EXACT_TILE runs.
-// n_ctx > 0 leaves out instantiations that cannot run that many keys.
-int resolve_exact(int64_t d, int causal, int dtype, int req_bm, int req_bn, int64_t n_ctx, const KernelEntry** out) {
+// and BN; ties go to the larger BN).  This is what a launch with a request runs.
+int resolve_exact(int64_t d, int causal, int dtype, int req_bm, int req_bn, const KernelEntry** out) {
     const int st = validate_request(causal, req_bm, req_bn);
     if (st != RSFA_OK) return st;
     const KernelEntry* best = nullptr;
     double best_dist = 0.0;
     for_each_kernel([&](const KernelEntry& e) {
         if (e.dtype != dtype || e.d != d || e.causal != (causal ? 1 : 0) || e.mode != MODE_FUSED) return;
-        if (n_ctx > 0 && !runs_shape(e, n_ctx)) return;
         const double dist = std::fabs(std::log2((double)e.bm / req_bm)) + std::fabs(std::log2((double)e.bn / req_bn));
         if (!best || dist < best_dist - 1e-9 || (std::fabs(dist - best_dist) <= 1e-9 && e.bn > best->bn)) {
             best = &e;
@@ -422,7 +407,7 @@ int rsfa_resolve_tiling(int64_t head_dim, int32_t causal, int32_t dtype, int32_t
     if (!valid_head_dim(head_dim)) return RSFA_E_HEADDIM;
     if (!valid_dtype(dtype)) return RSFA_E_DTYPE;
     const KernelEntry* e = nullptr;
-    const int st = resolve_exact(head_dim, causal, dtype, req_block_m, req_block_n, 0, &e);
+    const int st = resolve_exact(head_dim, causal, dtype, req_block_m, req_block_n, &e);
     if (st != RSFA_OK) return st;
     *block_m = e->bm;
     *block_n = e->bn;
@@ -454,18 +439,21 @@ uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t he
 }
 
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32_t block_m) {
-    (void)head_dim;
-    if (z < 1 || h < 1 || n_ctx < 1 || block_m < 1) return 0;
+    if (z < 1 || h < 1 || n_ctx < 1 || block_m < 1 || !valid_head_dim(head_dim)) return 0;
     const int64_t nmb = (n_ctx + block_m - 1) / block_m;
-    return (uint64_t)(2 * z * h * nmb * block_m) * sizeof(float);
+    // per query row: m and l, then the un-normalised accumulator (head_dim floats)
+    return (uint64_t)(z * h * nmb * block_m) * (uint64_t)(2 + head_dim) * sizeof(float);
 }
 
-// The tile a launch runs: the nearest compiled one for an exact request,
-// otherwise the tile search's choice for `num_cus` CUs (fwd_launch).
+// The tile a launch runs: for a request (block_m, block_n), the nearest
+// compiled one, as the reference's BLOCK_M / BLOCK_N select its kernel's
+// tile; under RSFA_FLAG_TILE_HINT (unless RSFA_FLAG_EXACT_TILE) and without a
+// request, the tile search's choice for `num_cus` CUs (fwd_launch).
 static int launch_tile(const rsfa_fwd_args* a, int num_cus, const KernelEntry** e) {
     const bool causal = a->causal != 0;
-    if ((a->flags & RSFA_FLAG_EXACT_TILE) && (a->block_m != 0 || a->block_n != 0))
-        return resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, a->n_ctx, e);
+    const bool hint = (a->flags & RSFA_FLAG_TILE_HINT) && !(a->flags & RSFA_FLAG_EXACT_TILE);
+    if ((a->block_m != 0 || a->block_n != 0) && !hint)
+        return resolve_exact(a->head_dim, causal, a->dtype, a->block_m, a->block_n, e);
     return choose_tiling(a->z, a->h, a->n_ctx, a->head_dim, causal, a->dtype, num_cus, e);
 }
 
@@ -519,9 +507,8 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     int num_cus = 0;
     if ((st = device_cus(ds, dev, &num_cus)) != RSFA_OK) return st;
 
-    // A valid (BLOCK_M, BLOCK_N) request is a hint, as it is a tuning knob of
-    // the reference: the launch runs the tile the search picks for the shape,
-    // unless RSFA_FLAG_EXACT_TILE asks for the nearest compiled one.
+    // A valid (BLOCK_M, BLOCK_N) request runs the nearest compiled tile, a
+    // hint (RSFA_FLAG_TILE_HINT) or no request the tile the search picks.
     const KernelEntry* e = nullptr;
     if ((st = launch_tile(a, num_cus, &e)) != RSFA_OK) return st;
     const int bm = e->bm;
@@ -559,7 +546,11 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
             v8_bytes + (split ? rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm) : 0);
         if (!ws || ws_bytes < need) return RSFA_E_WORKSPACE;
         if (((uintptr_t)ws & (v8_copy ? 15 : 3)) != 0) return RSFA_E_ALIGN;
-        if (split) p.state = (float*)((char*)ws + v8_bytes);
+        if (split) {
+            // (m, l) of every row, then the rows' fp32 accumulators
+            p.state = (float*)((char*)ws + v8_bytes);
+            p.acc = p.state + 2 * (int64_t)p.num_tasks * bm;
+        }
     }
     if (v8_copy) {
         uint32_t* wide = (uint32_t*)ws;

@@ -14,7 +14,12 @@ the same way and reported under ``"configs"``.
 Inputs follow the BASELINE recipe: Q, K, V ~ N(0, 1) drawn in fp32 by
 ``torch.Generator('cpu')`` from a per-config seed (q, k, v order), cast to
 fp16, copied to the GPU; their SHA-256 is compared with the committed
-fingerprints (tests/golden/input_fingerprints.json) where one exists.
+fingerprints (tests/golden/input_fingerprints.json) where one exists.  Every
+config's inputs are drawn and made resident before the first timing, and each
+config then gets the same steady state: about ``--device-warmup-s`` seconds of
+back-to-back launches (an idle GPU drops its clocks, and the first launches
+after a pause run below the steady rate), ``--warmup`` untimed calls, then
+``--steps`` timed calls.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
                     [--calibrate-copy-mib M] [--device-warmup-s S]
@@ -70,9 +75,9 @@ CAUSAL_TARGET = "C3"
 FINGERPRINTS = os.path.join(ROOT, "tests", "golden", "input_fingerprints.json")
 # fingerprint keys of configs that share a draw
 FINGERPRINT_KEY = {"C4-noncausal": "C4", "C4-causal": "C4"}
-# seconds of back-to-back launches before the first timed config: the clocks
-# start high and settle under sustained MFMA load
-DEVICE_WARMUP_S = 2.0
+# seconds of back-to-back launches before each timed config: an idle GPU
+# lowers its clocks, which then ramp and settle under sustained MFMA load
+DEVICE_WARMUP_S = 1.0
 
 
 def flops(B, H, S, D, causal):
@@ -85,10 +90,15 @@ def algo_bytes(B, H, S, D, causal, v_bytes=2):
     return (2.0 * 3 + v_bytes) * B * H * S * D + (0.0 if causal else 4.0 * B * H * S)
 
 
+def traffic_profile_path(name):
+    return os.path.join("profiles", f"fa_fwd_{name.lower().replace('-', '_')}_traffic.txt")
+
+
 def profile_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary of this workload, or None when there is none."""
-    path = os.path.join(ROOT, "profiles", f"fa_fwd_{name.lower().replace('-', '_')}_traffic.txt")
+    summary of this workload (not measured in this run: counters need their
+    own rocprofv3 passes), or None when there is none."""
+    path = os.path.join(ROOT, traffic_profile_path(name))
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -126,12 +136,19 @@ def fingerprint_check(torch, name, tensors):
     return h.hexdigest() == want
 
 
-def time_config(F, torch, cfg, steps, warmup, device_warmup_s=0.0, keep_cpu=False):
+def resident_inputs(torch, cfg, keep_cpu=False):
+    """The config's seeded inputs on the GPU, their fingerprint verdict, and
+    (keep_cpu) the CPU copies for the CPU baseline."""
+    q_c, k_c, v_c = make_inputs(torch, cfg)
+    fp_ok = fingerprint_check(torch, cfg[0], (q_c, k_c, v_c))
+    dev = (q_c.cuda(), k_c.cuda(), v_c.cuda())
+    return dev, fp_ok, ((q_c, k_c, v_c) if keep_cpu else None)
+
+
+def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0):
     name, B, H, S, D, causal, scale, seed = cfg[:8]
     v8 = len(cfg) > 8 and cfg[8] == "e5m2"
-    q_c, k_c, v_c = make_inputs(torch, cfg)
-    fp_ok = fingerprint_check(torch, name, (q_c, k_c, v_c))
-    q, k, v = q_c.cuda(), k_c.cuda(), v_c.cuda()
+    q, k, v = inputs
     BM, BN = F.get_tiling(B, H, S, D, causal)
     if device_warmup_s > 0:
         torch.cuda.synchronize()
@@ -154,8 +171,6 @@ def time_config(F, torch, cfg, steps, warmup, device_warmup_s=0.0, keep_cpu=Fals
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / steps
     fl = flops(B, H, S, D, causal)
-    del q, k, v
-    torch.cuda.empty_cache()
     res = {
         "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "seed": seed, "tiling": [BM, BN],
         "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
@@ -165,16 +180,31 @@ def time_config(F, torch, cfg, steps, warmup, device_warmup_s=0.0, keep_cpu=Fals
         "inputs_match_fingerprint": fp_ok,
         **({"v_dtype": "float8_e5m2"} if v8 else {}),
     }
-    return res, ((q_c, k_c, v_c) if keep_cpu else None)
+    return res
 
 
 def roofline(cfg, res):
-    """MFMA roofline of one config's kernel: algorithmic FLOPs per launch over
-    the average launch duration of the timed region."""
-    achieved = flops(*cfg[1:6]) / (res["ms_per_call"] * 1e-3) / 1e12
+    """Roofline of one config's kernel over the average launch duration of the
+    timed region.  The bound is the larger of the two floors: the algorithmic
+    FLOPs at the MFMA peak, or the algorithmic bytes (Q, K, V read once, O and
+    the LSE written once) at the HBM peak; ``achieved`` and ``frac`` are in
+    that bound's unit."""
+    B, H, S, D, causal = cfg[1:6]
+    v8 = len(cfg) > 8 and cfg[8] == "e5m2"
+    sec = res["ms_per_call"] * 1e-3
+    fl, by = flops(B, H, S, D, causal), algo_bytes(B, H, S, D, causal, 1 if v8 else 2)
     peak = peak_tflops(cfg)
+    traffic = profile_traffic(cfg[0])
+    src = {"traffic_source": traffic_profile_path(cfg[0]) + " (committed rocprofv3 FETCH_SIZE/WRITE_SIZE "
+                                                          "summary, not measured in this run)"} if traffic else {}
+    if by / (PEAK_HBM_GBS * 1e9) > fl / (peak * 1e12):
+        achieved = by / sec / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, **src,
+                "mfma_tflops": round(fl / sec / 1e12, 1)}
+    achieved = fl / sec / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": profile_traffic(cfg[0])}
+            "frac": round(achieved / peak, 4), "traffic": traffic, **src}
 
 
 def calibrate_copy(torch, mib):
@@ -259,7 +289,7 @@ def main():
     ap.add_argument("--only", default=None, help="time only this config name")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0)
     ap.add_argument("--device-warmup-s", type=float, default=DEVICE_WARMUP_S,
-                    help="seconds of back-to-back launches before the first config (0 under counter passes)")
+                    help="seconds of back-to-back launches before each config (0 under counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the path shards by (batch, head) with no "
@@ -275,22 +305,34 @@ def main():
         raise SystemExit(f"{_native.library_path()} is not built: run `python __graft_entry__.py build` first")
     torch.cuda.set_device(0)
     configs = [c for c in CONFIGS if args.only in (None, c[0])]
-    results = {}
-    head_inputs = None
+    # every config's inputs resident before the first timing (configs that
+    # share a draw share the tensors)
+    resident, head_inputs = {}, None
     for i, cfg in enumerate(configs):
-        keep = i == 0 and not args.no_cpu
-        results[cfg[0]], kept = time_config(F, torch, cfg, args.steps, args.warmup,
-                                            device_warmup_s=args.device_warmup_s if i == 0 else 0.0, keep_cpu=keep)
-        if keep:
-            head_inputs = kept
+        key = FINGERPRINT_KEY.get(cfg[0], cfg[0]) + ("-" + cfg[8] if len(cfg) > 8 else "")
+        if key not in resident:
+            dev, fp_ok, kept = resident_inputs(torch, cfg, keep_cpu=(i == 0 and not args.no_cpu))
+            resident[key] = (dev, fp_ok)
+            if kept is not None:
+                head_inputs = kept
+        print(f"[bench] inputs of {cfg[0]} resident", file=sys.stderr, flush=True)
+    results = {}
+    for cfg in configs:
+        key = FINGERPRINT_KEY.get(cfg[0], cfg[0]) + ("-" + cfg[8] if len(cfg) > 8 else "")
+        dev, fp_ok = resident[key]
+        results[cfg[0]] = time_config(F, torch, cfg, dev, fp_ok, args.steps, args.warmup,
+                                      device_warmup_s=args.device_warmup_s)
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
+    resident.clear()
+    torch.cuda.empty_cache()
     if args.calibrate_copy_mib:
         calibrate_copy(torch, args.calibrate_copy_mib)
     cfg = configs[0]
     r = results[cfg[0]]
     by_name = {c[0]: c for c in configs}
     for name, res in results.items():
-        res["roofline_frac"] = roofline(by_name[name], res)["frac"]
+        rf = roofline(by_name[name], res)
+        res["roofline_bound"], res["roofline_frac"] = rf["bound"], rf["frac"]
     line = {
         "metric": METRIC,
         "value": r["tflops"],

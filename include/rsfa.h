@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define RSFA_ABI_VERSION 4
+#define RSFA_ABI_VERSION 5
 
 typedef enum rsfa_status {
     RSFA_OK          = 0,
@@ -88,12 +88,16 @@ typedef enum rsfa_dtype {
                                           dynamic atomic-ticket queue            */
 #define RSFA_FLAG_CAUSAL_SPLIT    0x2u /* causal only: two launches, mask-free
                                           prefix then masked diagonal, with the
-                                          (m, l, acc) state handed over through
-                                          `workspace` (reference 493-541)       */
-#define RSFA_FLAG_EXACT_TILE      0x4u /* run the compiled tile nearest to
-                                          (block_m, block_n) instead of the
-                                          tile rsfa_get_tiling picks (used to
-                                          time or test one instantiation)       */
+                                          (m, l, acc) state handed over in fp32
+                                          through `workspace` (reference
+                                          493-541)                              */
+#define RSFA_FLAG_EXACT_TILE      0x4u /* a request (block_m, block_n) runs the
+                                          compiled tile nearest to it: the
+                                          default, kept for callers of ABI
+                                          version 4; overrides TILE_HINT        */
+#define RSFA_FLAG_TILE_HINT       0x8u /* a valid request is only checked, and
+                                          the tile rsfa_get_tiling picks for
+                                          the shape runs                        */
 
 typedef struct rsfa_fwd_args {
     uint32_t    struct_size;  /* = sizeof(rsfa_fwd_args)                        */
@@ -117,11 +121,14 @@ typedef struct rsfa_fwd_args {
     float       sm_scale;     /* multiplies q.k before the softmax              */
     int32_t     causal;       /* 0/1: key n visible to query m iff n <= m       */
     int32_t     block_m;      /* requested BLOCK_M; 0 (with block_n 0) = no
-                                 request.  A request is checked against the
-                                 reference's rules (RSFA_E_TILE otherwise) and
-                                 is a hint, like the reference's tuning knob:
-                                 the launch runs the tile rsfa_get_tiling picks
-                                 for the shape, unless RSFA_FLAG_EXACT_TILE    */
+                                 request, the tile rsfa_get_tiling picks runs.
+                                 A request is checked against the reference's
+                                 rules (RSFA_E_TILE otherwise) and, like the
+                                 reference's BLOCK_M/BLOCK_N meta-parameters,
+                                 selects the tile: the compiled one nearest to
+                                 it runs (rsfa_resolve_tiling), unless
+                                 RSFA_FLAG_TILE_HINT.  Split mode sizes its
+                                 workspace with the BLOCK_M that runs        */
     int32_t     block_n;      /* requested BLOCK_N (see block_m)                */
     uint32_t    flags;        /* RSFA_FLAG_*                                    */
 } rsfa_fwd_args;
@@ -151,8 +158,12 @@ int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
 int rsfa_attention_fwd_noalloc(const rsfa_fwd_args *args, void *stream);
 
 /* Bytes of fp32 workspace RSFA_FLAG_CAUSAL_SPLIT needs for this problem and
- * tiling (the reference allocates state[2, Z, H, NBM, BM] at 501; this library
- * also keeps the un-normalised accumulator in fp32 instead of fp16 in O). */
+ * the BLOCK_M that runs (rsfa_resolve_tiling of the request, or
+ * rsfa_get_tiling's without one / under RSFA_FLAG_TILE_HINT): state[2, Z, H,
+ * NBM, BM] (row max in exp2 units, row sum), as the reference allocates at
+ * 501, then the un-normalised accumulator [Z, H, NBM, BM, head_dim] in fp32,
+ * which the reference instead rounds to the input dtype into O (353).
+ * 0 for invalid sizes. */
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                     int64_t head_dim, int32_t block_m);
 
@@ -173,7 +184,8 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim,
                     int32_t *block_n);
 
 /* Maps a caller-requested (BLOCK_M, BLOCK_N) to the compiled instantiation
- * that runs it under RSFA_FLAG_EXACT_TILE (the nearest compiled tile).
+ * a launch with that request runs (the nearest compiled tile; log distance
+ * in BLOCK_M and BLOCK_N, ties to the larger BLOCK_N).
  * Requests follow the reference's rules (powers of two,
  * 16 <= BLOCK <= 512, BLOCK_M*BLOCK_N <= 65536, causal needs
  * BLOCK_N <= BLOCK_M, which the reference silently breaks on, see

@@ -63,3 +63,21 @@ def test_cpu_baseline_reports_cores_and_model():
     assert cb["kind"] == "port" and cb["unit"] == "TFLOP/s" and cb["value"] > 0
     assert cb["cores"] == bench.host_threads() >= 1 and cb["os_cpu_count"] == os.cpu_count()
     assert isinstance(cb["cpu_model"], str) and cb["cpu_model"]
+
+
+def test_roofline_bound_is_the_larger_floor():
+    by_name = {c[0]: c for c in bench.CONFIGS}
+    # C4-causal (64,8,1024,256): 2.75e11 FLOP at 2.5 PFLOP/s = 0.110 ms, below its
+    # 1.07 GB at 8 TB/s = 0.134 ms: HBM-bound, reported in GB/s
+    c4c = by_name["C4-causal"]
+    rf = bench.roofline(c4c, {"ms_per_call": 0.268})
+    assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == bench.PEAK_HBM_GBS
+    assert abs(rf["achieved"] - bench.algo_bytes(64, 8, 1024, 256, True) / 0.268e-3 / 1e9) < 0.1
+    assert abs(rf["frac"] - rf["achieved"] / bench.PEAK_HBM_GBS) < 1e-4
+    # the target (1024 FLOP/B) is MFMA-bound, in TFLOP/s
+    rt = bench.roofline(by_name["target-noncausal"], {"ms_per_call": 2.0})
+    assert rt["bound"] == "mfma" and rt["unit"] == "TFLOP/s"
+    assert abs(rt["achieved"] - bench.flops(128, 8, 2048, 128, False) / 2.0e-3 / 1e12) < 0.1
+    # a traffic figure names the committed profile it comes from
+    if rt["traffic"] is not None:
+        assert "not measured in this run" in rt["traffic_source"]

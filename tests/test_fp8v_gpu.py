@@ -167,9 +167,9 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
 
 
 @pytest.mark.parametrize("N", [64, 1024])
-def test_pipelined_tile_within_the_rounding_bound(N):
-    """A (256, 32) tile request with a float8 V at head dim 128: the pipelined
-    kernel of that tile has no byte-V variant, so the nearest byte-V tile runs."""
+def test_uncompiled_tile_request_within_the_rounding_bound(N):
+    """A (256, 32) tile request with a float8 V at head dim 128, a tile no
+    head-dim-128 kernel has: the nearest compiled byte-V tile runs."""
     Z, H, D = 1, 4, 128
     q, k, v = A.make_inputs(Z, H, N, D, seed=N + 3)
     v8 = v.to(torch.float8_e5m2)
@@ -252,3 +252,108 @@ def test_float8_v_lse_is_the_exact_logsumexp(D, causal):
     got = torch.stack([lse[z, h].cpu() for z, h in heads])
     assert torch.isfinite(got).all()
     assert (got - ref_lse).abs().max().item() < 1e-3
+
+
+def _byte_tiles(D, causal):
+    """The compiled tiles a float8 V can run at head dim D (each reached by
+    the request nearest to it)."""
+    reqs = [(256, 128), (256, 64), (256, 32), (128, 64), (128, 32)]
+    return sorted({tuple(faf.resolve_tiling(D, causal, bm, bn)) for bm, bn in reqs if not (causal and bn > bm)})
+
+
+def _peaked_inputs(N, D, causal, seed):
+    """Query i attends to key pi(i) alone: K rows are random +-1, Q[i] =
+    K[pi(i)], and sm_scale 1, so the score of pi(i) is D while every other
+    visible key scores at most D - 30 / log2(e) (checked here in float64):
+    every other P is below 2^-30 of P[pi(i)] = 1.  V rows are distinct e5m2
+    values, so O[i] = V[pi(i)] exactly names the key the kernel paired with
+    row i.  Non-causal pi is a permutation (every key position of every
+    64-key MFMA group and tile once); causal pi(i) in [i - 63, i]."""
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randint(0, 2, (N, D), generator=g) * 2 - 1).float()
+    if causal:
+        pi = torch.tensor([i - int(torch.randint(0, min(i, 63) + 1, (1,), generator=g)) for i in range(N)])
+    else:
+        pi = torch.randperm(N, generator=g)
+    q = k[pi]
+    s = (q.double() @ k.double().T)
+    if causal:
+        s.masked_fill_(A.causal_mask(N), float("-inf"))
+    top = s.gather(1, pi[:, None]).squeeze(1)
+    others = s.scatter(1, pi[:, None], float("-inf")).max(dim=1).values
+    assert bool((top == D).all()) and bool(((top - others) * 1.4426950408889634 >= 30).all()), \
+        "construction: a row's peak is not 30 log2 units above its other keys"
+    v8 = torch.from_numpy(A.round_e5m2((torch.randn(N, D, generator=g) * 2).numpy())).to(torch.float8_e5m2)
+    assert len({tuple(r) for r in v8.view(torch.uint8).tolist()}) == N, "V rows must be distinct"
+    return q.half()[None, None], k.half()[None, None], v8[None, None], pi
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [64, 273, 1024])
+def test_peaked_rows_return_their_key_value_on_every_tile(D, causal, N):
+    """Known answers for the float8 V P.V path on every compiled tile: head
+    dims 64 and 128 read V's bytes (byte-transposing reads, swizzled 16-byte
+    chunks, P and V paired byte by byte inside each 64-key MFMA), head dim
+    256 its fp16 copy.  A key read from the wrong row, chunk, lane or 16-key
+    group gives another row's V."""
+    q, k, v8, pi = _peaked_inputs(N, D, causal, seed=1000 + N + D + causal)
+    want = v8[0, 0].float()[pi]
+    for tile in _byte_tiles(D, causal):
+        o = _run(q, k, v8, causal, 1.0, BM=tile[0], BN=tile[1])[0, 0]
+        bad = (o - want).abs() > 2.0 ** -10 * want.abs()
+        assert not bool(bad.any()), (f"tile {tile}: {int(bad.any(dim=1).sum())} of {N} rows differ from "
+                                     f"V[pi(i)], first row {int(bad.any(dim=1).nonzero()[0])}")
+
+
+def _first_key_max_inputs(Z, H, N, D, seed):
+    """Inputs whose kernel P is exactly the oracle's: key 0 carries every
+    row's largest score, so the running max is the exact row max from the
+    first key tile on (no lagging max), and every score is a multiple of 1/8
+    (Q in {0, +-1/2}, K in {0, +-1/4}: exact in fp16 and in fp32 sums), so
+    with sm_scale = ln 2 each P = 2^(-j/8).  Those values lie at least 1.7 %
+    from every rounding midpoint of e5m2, so the kernel's exp2 and the
+    oracle's float64 exp round them alike.  Coordinate 0 is reserved: Q[:, 0]
+    = 1, K[j, 0] = 0 for j > 0, K[0, 0] = B, the smallest multiple of 1/4
+    that puts key 0 at least 1/8 above each row's other keys.  One P value is
+    an e5m2 tie, 2^-17 (half the smallest subnormal): draws where a score
+    sits exactly 17 below its row max are skipped (the next draw of the
+    seed's sequence is taken).  V ~ N(0, 1) rounded to e5m2."""
+    g = torch.Generator().manual_seed(seed)
+    for _ in range(64):
+        q = (torch.randint(-1, 2, (Z, H, N, D), generator=g) * 0.5).float()
+        k = (torch.randint(-1, 2, (Z, H, N, D), generator=g) * 0.25).float()
+        q[..., 0] = 1.0
+        k[..., 0] = 0.0
+        s = q.double() @ k.double().transpose(-1, -2)
+        need = (s[..., 1:].max(dim=-1).values - s[..., 0]).max().item() + 0.125
+        k[:, :, 0, 0] = float(np.ceil(max(need, 0.0) * 4) / 4)
+        s = q.double() @ k.double().transpose(-1, -2)
+        if not bool((s - s[..., :1] == -17.0).any()):
+            break
+    else:
+        raise AssertionError("construction: no draw without an e5m2 tie")
+    v8 = torch.from_numpy(A.round_e5m2(torch.randn(Z, H, N, D, generator=g).numpy())).to(torch.float8_e5m2)
+    return q.half(), k.half(), v8
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("N", [200, 1000])
+def test_exact_row_max_matches_the_rounded_p_oracle(D, causal, N):
+    """With the row max on key 0 and scores on a 1/8 grid the kernel rounds
+    exactly the P the oracle rounds (reference_attention_fp8v: P = 2^(-j/8),
+    1 -> 1, 0.917 -> 0.875, ...), so O must match it to fp16 rounding, not
+    just within the loose per-element rounding bound: on the byte tiles
+    (D = 64, 128) and the fp16-copy path (D = 16, 32, 256), at lengths whose
+    last 64-key group is partial."""
+    Z, H = 1, 2
+    q, k, v8 = _first_key_max_inputs(Z, H, N, D, seed=2000 + N + D)
+    scale = float(np.log(2.0))
+    heads = [(0, 0), (0, H - 1)]
+    want = A.reference_attention_fp8v(q, k, v8, causal, scale, heads=heads)
+    for tile in _byte_tiles(D, causal):
+        o = _run(q, k, v8, causal, scale, BM=tile[0], BN=tile[1])
+        got = torch.stack([o[z, h] for z, h in heads])
+        excess = ((got - want).abs() - (1e-4 + 2.0 ** -10 * want.abs())).max().item()
+        assert excess <= 0, f"tile {tile}: outside fp16 rounding of the exact-P oracle by {excess:.3e}"

@@ -116,11 +116,14 @@ def test_resolve_tiling_rules(req, causal, ok):
 
 
 def test_split_workspace_bytes_matches_reference_state_shape():
-    # reference: state = empty((2, Z, H, cdiv(N, BM), BM), fp32)  (flash_attention_forward.py:501)
+    # reference: state = empty((2, Z, H, cdiv(N, BM), BM), fp32)  (flash_attention_forward.py:501),
+    # then the un-normalised accumulator [Z, H, cdiv(N, BM), BM, D] in fp32, which the
+    # reference rounds to the input dtype into O instead (353)
     lib = _native.lib()
-    assert lib.rsfa_split_workspace_bytes(128, 8, 2048, 128, 128) == 2 * 128 * 8 * 16 * 128 * 4
-    assert lib.rsfa_split_workspace_bytes(2, 3, 100, 64, 64) == 2 * 2 * 3 * 2 * 64 * 4
+    assert lib.rsfa_split_workspace_bytes(128, 8, 2048, 128, 128) == (2 + 128) * 128 * 8 * 16 * 128 * 4
+    assert lib.rsfa_split_workspace_bytes(2, 3, 100, 64, 64) == (2 + 64) * 2 * 3 * 2 * 64 * 4
     assert lib.rsfa_split_workspace_bytes(0, 3, 100, 64, 64) == 0
+    assert lib.rsfa_split_workspace_bytes(2, 3, 100, 48, 64) == 0
 
 
 def test_v8_workspace_bytes_is_the_fp16_copy_of_v():
@@ -179,7 +182,7 @@ def _valid_args(**over):
     (dict(dtype=3), _native.E_DTYPE),
     # a float8 V needs 16-byte rows: outer strides a multiple of 16 elements
     (dict(dtype=_native.DTYPE_F16_V8E5M2, v_stride=[3 * 128 * 72, 128 * 72, 72, 1]), _native.E_ALIGN),
-    # tile requests follow the reference's rules even though they are hints
+    # tile requests follow the reference's rules
     (dict(block_m=48, block_n=64), _native.E_TILE),
     (dict(block_m=64, block_n=256, causal=1), _native.E_TILE),
     # K/V row strides whose 128-row key tile (D=64) spans 4 GiB: the loader's
@@ -210,7 +213,7 @@ def test_attention_fwd_without_gpu_reports_device_error():
     dict(q_stride=[0, 0, 16909312, 1]),
     dict(head_dim=256, k_stride=[0, 0, 69273656, 1]),
     dict(z=1024, h=1024, n_ctx=2048, causal=1),     # fused causal has no split-state limit
-    dict(block_m=128, block_n=64, causal=1),        # a valid request (a hint)
+    dict(block_m=128, block_n=64, causal=1),        # a valid request
 ])
 def test_attention_fwd_limits_admit_the_boundary(over):
     """Arguments just inside the index limits pass every check made before

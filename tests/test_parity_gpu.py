@@ -3,9 +3,10 @@
 Tolerance: atol = rtol = 1e-2 against fp32 softmax(q k^T * scale) v on the same
 fp16/bf16 inputs (the reference's own allclose at
 benchmarks/run_correctness_test.py:148 and flash_attention_forward.py:736-738).
-At the BASELINE configs' full sizes every head is checked for size-independent
-properties (finite, inside the convex hull of V) and a seeded sample of heads
-against the oracle.
+At the BASELINE configs' full sizes every head is checked: for size-independent
+properties (finite, inside the convex hull of V), against a chunked fp32 torch
+reference on the GPU, and a seeded sample of heads against the CPU oracle, which
+also checks the GPU reference.
 """
 import json
 import math
@@ -58,6 +59,32 @@ def _sample_heads(Z, H, count, seed):
     return [(i // H, i % H) for i in sorted(idx)]
 
 
+def _gpu_reference(qd, kd, vd, causal, scale):
+    """fp32 softmax(q k^T * scale) v of every head on the GPU, chunked so a
+    chunk's scores take at most 1 GiB.  Test infrastructure beside the CPU
+    oracle (the same closed form), which checks it on sampled heads."""
+    Z, H, N, D = qd.shape
+    G = Z * H
+    q, k, v = (t.reshape(G, N, D) for t in (qd, kd, vd))
+    out = torch.empty((G, N, D), dtype=torch.float32, device=qd.device)
+    mask = torch.triu(torch.ones(N, N, dtype=torch.bool, device=qd.device), 1) if causal else None
+    step = max(1, (1 << 30) // (N * N * 4))
+    allow = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False  # full fp32 products
+    try:
+        for g0 in range(0, G, step):
+            g1 = min(G, g0 + step)
+            kt = k[g0:g1].float().transpose(-1, -2).contiguous()
+            s = torch.bmm(q[g0:g1].float(), kt) * float(scale)
+            if causal:
+                s.masked_fill_(mask, float("-inf"))
+            out[g0:g1] = torch.bmm(torch.softmax(s, dim=-1), v[g0:g1].float())
+            del s, kt
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = allow
+    return out.reshape(Z, H, N, D)
+
+
 def _convex_hull_ok(out, v, causal):
     of = out.float()
     vf = v.float()
@@ -90,7 +117,18 @@ def test_baseline_configs(cfg):
     ref = A.reference_attention(q, k, v, causal, scale, heads=heads)
     got = torch.stack([out[z, h] for z, h in heads])
     err = _assert_close(got, ref, name)
-    print(f"{name}: tiling {BM}x{BN}, max |err| on {len(heads)} heads = {err:.3e}")
+    # every head against the GPU reference, itself checked against the oracle
+    gref = _gpu_reference(qd, kd, vd, causal, scale)
+    gsample = torch.stack([gref[z, h] for z, h in heads]).cpu()
+    assert (gsample - ref).abs().max().item() < 1e-4, "GPU fp32 reference disagrees with the oracle"
+    of = out.float()
+    bad = ~((of - gref).abs() <= ATOL + RTOL * gref.abs())
+    assert not bool(bad.any()), (f"{name}: {int(bad.any(dim=-1).any(dim=-1).sum())} of {Z * H} heads outside "
+                                 f"atol=rtol=1e-2, max |err| {(of - gref).abs().max().item():.3e}")
+    err_all = (of - gref).abs().max().item()
+    del gref, of
+    print(f"{name}: tiling {BM}x{BN}, max |err| on {len(heads)} heads (oracle) = {err:.3e}, "
+          f"on all {Z * H} heads (GPU fp32 reference) = {err_all:.3e}")
 
 
 # The reference's own parametrisation of test_op (flash_attention_forward.py:668-699),
@@ -131,14 +169,14 @@ def test_reference_test_op_cases(Z, H, N_CTX, HEAD_DIM, causal, dtype, BM, BN):
     qd.requires_grad_()
     kd.requires_grad_()
     vd.requires_grad_()
-    # the request as a hint (the drop-in path: get_tiling's tile runs), then
-    # the compiled tile nearest to it
+    # the reference's call (the compiled tile nearest to the request runs),
+    # then the request as a hint (get_tiling's tile runs)
     out = F.attention(qd, kd, vd, causal, 0.5, BM, BN).to(dtype)
-    exact = F.forward(qd.detach(), kd.detach(), vd.detach(), causal, 0.5, BM, BN, exact_tile=True)
+    hint = F.forward(qd.detach(), kd.detach(), vd.detach(), causal, 0.5, BM, BN, tile_hint=True)
     torch.cuda.synchronize()
     heads = _sample_heads(Z, H, 32, 7)
     ref = A.reference_attention(q, k, v, causal, 0.5, heads=heads)
-    for label, o in (("hint", out), ("exact", exact)):
+    for label, o in (("request", out), ("hint", hint)):
         got = torch.stack([o.detach()[z, h] for z, h in heads])
         _assert_close(got, ref, f"test_op{(Z, H, N_CTX, HEAD_DIM, causal, dtype, BM, BN)} {label}")
 
@@ -299,7 +337,9 @@ def test_causal_two_launch_split_matches_fused(BM, BN):
     ref = A.reference_attention(q, k, v, True, 0.125)
     _assert_close(fused, ref, "fused")
     _assert_close(split, ref, "split")
-    assert (fused.float() - split.float()).abs().max().item() < 5e-3
+    # fp32 hand-off between the launches: the two differ by the final
+    # rounding of O at most (|O| < 1, fp16 ulp 2^-11 below 1)
+    assert (fused.float() - split.float()).abs().max().item() <= 2.0 ** -10
 
 
 def test_many_launches_across_streams():
@@ -336,10 +376,11 @@ def test_causal_diagonal_in_pingpong_matches_masked_body(dtype, N):
     ref = A.reference_attention(q, k, v, True, 0.3)
     _assert_close(fused, ref, f"fused N={N}")
     _assert_close(split, ref, f"split N={N}")
-    # the split rounds the prefix's O to the input dtype between its launches
-    # (reference :353): a few units in the last place of bf16 apart at most
-    tol = 5e-3 if dtype == torch.float16 else 4e-2
-    assert (fused.float() - split.float()).abs().max().item() < tol
+    # the split hands (m, l, acc) over in fp32 (the reference rounds acc to
+    # the input dtype into O, :353), so the two differ only by the final
+    # rounding of O: one unit in the last place of |O| < 1 at most
+    ulp = 2.0 ** (-10 if dtype == torch.float16 else -7)
+    assert (fused.float() - split.float()).abs().max().item() <= ulp
     # row 0 of every head sees key 0 only
     assert torch.allclose(fused[:, :, 0].float().cpu(), v[:, :, 0].float(), atol=2e-3)
 
@@ -390,34 +431,6 @@ def test_many_heads_short_rows(causal):
     heads = [(0, 0), (1023, 17), (Z - 1, H - 1)]
     ref = A.reference_attention(q, k, v, causal, 0.2, heads=heads)
     _assert_close(torch.stack([out[z, h] for z, h in heads]), ref, "many heads")
-
-
-@pytest.mark.parametrize("N", [32, 64, 96, 288, 1024, 2048])
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_pipelined_tile_256x32(N, dtype):
-    """The software-pipelined kernel (tile (256, 32): 8 waves of 32 rows, the
-    softmax of key tile t+1 interleaved with the MFMAs of tile t+2 and t, one
-    barrier per pair of key tiles), D=128 non-causal, with its LSE, against the
-    oracle.  N covers one key tile, the two- and three-step tails and the
-    steady loop."""
-    Z, H, D = 2, 3, 128
-    q, k, v = A.make_inputs(Z, H, N, D, seed=N + 7, dtype=dtype)
-    print(f"pipelined (256,32): N={N} {dtype}", flush=True)
-    out, lse = F.forward(*_to_gpu(q, k, v), False, 0.3, 256, 32, exact_tile=True, return_lse=True)
-    ref, ref_lse = A.reference_attention(q, k, v, False, 0.3, return_lse=True)
-    _assert_close(out, ref, f"pipelined N={N}")
-    assert (lse.cpu() - ref_lse).abs().max().item() < 1e-2
-
-
-@pytest.mark.parametrize("scale", [-0.4, 0.0, 2.0])
-def test_pipelined_tile_scales_and_strides(scale):
-    """Negative, zero and large scales (frequent rescales of O) on the
-    pipelined kernel, with BSHD-strided inputs."""
-    Z, H, N, D = 2, 4, 512, 128
-    q, k, v = A.make_inputs(Z, H, N, D, seed=99)
-    qd, kd, vd = (t.transpose(1, 2).contiguous().transpose(1, 2).to(DEV) for t in (q, k, v))
-    out = F.forward(qd, kd, vd, False, scale, 256, 32, exact_tile=True)
-    _assert_close(out, A.reference_attention(q, k, v, False, scale), f"pipelined scale={scale}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -172,7 +172,7 @@ def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     # at head dims 64 and 128 the kernels read a float8 V's bytes: no copy, any size
     assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 128) == 0
     big_v8 = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
-    # split state: 8 bytes per query row, rounded to the tile
+    # split state: (2 + head_dim) fp32 per query row, rounded to the tile
     split = _cpu_args(z=8, h=32, n_ctx=16384, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(split), None) == _native.E_SCRATCH
     assert "RSFA_NOALLOC_WORKSPACE_BYTES" in lib.rsfa_strerror(_native.E_SCRATCH).decode()
