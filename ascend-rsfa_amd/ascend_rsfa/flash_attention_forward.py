@@ -24,9 +24,9 @@ that are not on a GPU, the calls raise.
 
 A ``float8_e5m2`` V with float16 Q and K runs the reference's fp8_v branch
 (_attn_fwd_inner 208-211, 217): P is rounded to e5m2 for P.V while the row
-sums add the unrounded P; O is float16.  At head dims 64 and 128 the kernels
-read V's bytes and run P.V on the e5m2 MFMA; at head dims 16, 32 and 256 the
-library first widens V to fp16 in a workspace (exact: an e5m2 byte is the
+sums add the unrounded P; O is float16.  At head dims 64, 128 and 256 the
+kernels read V's bytes and run P.V on the e5m2 MFMA; at head dims 16 and 32
+the library first widens V to fp16 in a workspace (exact: an e5m2 byte is the
 high byte of that fp16) and P is rounded to e5m2 and widened back.
 
 ``BM``/``BN`` keep the reference's meaning (query rows per program, keys per

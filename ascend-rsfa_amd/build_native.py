@@ -39,8 +39,12 @@ HIPCC_FLAGS = [
     "-I" + os.path.join(REPO_ROOT, "include"),
 ]
 
-# Per-file flags (none at present; kept for instantiation units that need their own).
-FILE_FLAGS = {}
+# Per-file flags.  kern_d256.hip: MFMAs in the VGPR form (accumulators in
+# VGPRs) for its one-wave-per-SIMD float8-V tile, which has 512 registers:
+# left to choose, the compiler gives every MFMA an AGPR accumulator and the
+# softmax then copies each score out of the AGPRs.  The kernels built for two
+# waves per SIMD use no AGPRs either way and compile to the same code.
+FILE_FLAGS = {"kern_d256.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc():

@@ -424,16 +424,24 @@ fa_fwd_kernel(FwdParams p) {
     // c ^ v8_swz(R), so the eight rows one transposing read of P.V gathers
     // (below), and the sixteen (row, chunk) pairs of 32 lanes, fall in
     // distinct banks: R % 4 + 4 ((R / 8) % 2) for 128-byte rows (rows 2 apart
-    // share banks), 2 ((R / 8) % 2) for 64-byte rows (rows 4 apart do).
+    // share banks), 2 ((R / 8) % 2) for 64-byte rows (rows 4 apart do), and
+    // twice the 128-byte value for 256-byte rows (every row spans all banks,
+    // so the two chunk columns c, c ^ 1 one read takes from each of its eight
+    // rows must land on sixteen distinct columns).
     constexpr bool V8 = T::v8;
-    static_assert(!V8 || ((D == 64 || D == 128) && BN % 64 == 0), "byte V tiles: head dim 64 or 128, 64-key groups");
+    static_assert(!V8 || ((D == 64 || D == 128 || D == 256) && (BN % 64 == 0 || BN == 32)),
+                  "byte V tiles: head dim 64, 128 or 256; 64-key groups or one 32-key tile");
     constexpr int TILEV = V8 ? BN * D : TILE;  // bytes of one V tile
     constexpr int BUF = TILE + TILEV;          // K + V
     constexpr int NINSTV = V8 ? TILEV / 1024 : NINST;
     constexpr int V8RPS = 1024 / DP;           // rows per 1-KB slice of a byte V tile
     constexpr int V8CPR = DP / 16;             // 16-byte chunks per row of it
     // (rq = R % 4, rh = (R / 8) % 2 of the row)
-    auto v8_swz = [](int rq, int rh) { return D == 64 ? 2 * rh : rq + 4 * rh; };
+    auto v8_swz = [](int rq, int rh) { return D == 64 ? 2 * rh : D == 128 ? rq + 4 * rh : 2 * (rq + 4 * rh); };
+    // V8: transposing reads per float8 MFMA (64 keys): four, or two for a
+    // 32-key tile, whose MFMA takes P = 0 for its upper 32 keys (and the same
+    // two reads again as their finite V)
+    constexpr int V8RPM = 2 * NKT < 4 ? 2 * NKT : 4;
     static_assert(BN % 32 == 0 && BN >= 32, "BN must be a multiple of 32");
     static_assert(D % 16 == 0, "D must be a multiple of 16");
     static_assert((BN * CPR) % 64 == 0, "tile must be whole 1-KB load slices");
@@ -525,14 +533,34 @@ fa_fwd_kernel(FwdParams p) {
     // (P^T, in the S^T accumulator layout); so row r of the group is that key
     // for e = r, and the group's 16 columns are head dims 32db + 16((lane /
     // 16) % 2) ...  Offset from the tile at q' = 0 (q' adds 16q' rows), per db.
-    uint32_t vo8[V8 ? DT : 1];
+    // At D = 256 (eight head-dim blocks, O^T and Q^T in 192 VGPRs) only the
+    // row base and swizzle are kept (v8_rb, v8_sw) and each block's offset is
+    // formed where it is read (v8_off).
+    constexpr bool V8_INLINE = V8 && DT > 4;
+    uint32_t vo8[V8 && !V8_INLINE ? DT : 1];
+    int v8_rb = 0, v8_sw = 0;
     if constexpr (V8) {
         const int tr = l16 >> 1;  // row r of the group: R % 4 = r % 4, (R / 8) % 2 = r / 4
         const int rowb = D * (4 * hh + (tr & 3) + 8 * (tr >> 2)) + 8 * (l16 & 1);
         const int swz = v8_swz(tr & 3, tr >> 2);
+        if constexpr (V8_INLINE) {
+            v8_rb = rowb;
+            v8_sw = swz ^ ((lane >> 4) & 1);  // (2 db + g) ^ swz = 2 db ^ (swz ^ g)
+        } else {
 #pragma unroll
-        for (int db = 0; db < DT; ++db) vo8[db] = (uint32_t)(rowb + 16 * ((2 * db + ((lane >> 4) & 1)) ^ swz));
+            for (int db = 0; db < DT; ++db) vo8[db] = (uint32_t)(rowb + 16 * ((2 * db + ((lane >> 4) & 1)) ^ swz));
+        }
     }
+    // byte offset of head-dim block db's transposing reads from a V tile
+    auto v8_off = [&](int db) -> uint32_t {
+        if constexpr (V8_INLINE) {
+            int sw = v8_sw;
+            asm volatile("" : "+v"(sw));  // formed here, not hoisted out of the loops
+            return (uint32_t)(v8_rb + 16 * ((2 * db) ^ sw));
+        } else {
+            return vo8[db];
+        }
+    };
 
     // Loader: in every 1-KB slice lane i fills chunk 4*cg + i/16 of the 16-row
     // block's row (i%16) ^ 4*((i/16)%4), so its global offset inside the block
@@ -1008,29 +1036,35 @@ fa_fwd_kernel(FwdParams p) {
             if constexpr (V8) {
                 // read i = (d*NKT + kt)*2 + h2 fetches keys 16(2kt + h2).. of
                 // head-dim block d (byte-transposing, 8 bytes per lane); every
-                // fourth completes the A operand of a 64-key float8 MFMA, whose
-                // B operand is sub-tiles 2kk, 2kk+1 of the P bytes
+                // V8RPM-th completes the A operand of a 64-key float8 MFMA, whose
+                // B operand is sub-tiles 2kk, 2kk+1 of the P bytes (P = 0 past
+                // a 32-key tile)
                 constexpr int NM = DT * NKT * 2;
-                constexpr int PF = 8;       // two float8 MFMAs ahead
-                constexpr int NB = PF + 4;  // the four reads of an MFMA stay live to it
+                constexpr int PF = V8RPM == 2 ? 4 : 8;  // two float8 MFMAs ahead
+                constexpr int NB = PF + V8RPM;  // the reads of an MFMA stay live to it
                 const uint32_t vb = smem_addr + vofs;
                 if (!MASK) {
                     i32x2 rv[NB];
                     auto issue = [&](auto ic) {
                         constexpr int i = decltype(ic)::value;
                         constexpr int d = i / (2 * NKT), kt = (i / 2) % NKT, h2 = i % 2;
-                        rv[i % NB] = lds_read_tr8<(2 * kt + h2) * 16 * D>(vb + vo8[d]);
+                        rv[i % NB] = lds_read_tr8<(2 * kt + h2) * 16 * D>(vb + v8_off(d));
                     };
                     static_for<PF>(issue);
                     static_for<NM>([&](auto ic) {
                         constexpr int i = decltype(ic)::value;
                         constexpr int d = i / (2 * NKT), qq = i % (2 * NKT);
                         constexpr int ahead = (NM - 1 - i) < (PF - 1) ? (NM - 1 - i) : (PF - 1);
-                        if constexpr (qq % 4 == 3) {
+                        if constexpr (V8RPM == 4 && qq % 4 == 3) {
                             i32x2 &r0 = rv[(i - 3) % NB], &r1 = rv[(i - 2) % NB], &r2 = rv[(i - 1) % NB], &r3 = rv[i % NB];
                             lgkm_wait4<ahead>(r0, r1, r2, r3);
                             o[d] = T::mfma8(cat4(r0, r1, r2, r3), cat2(pk[qq / 2 - 1][0], pk[qq / 2][0]), o[d]);
                             __builtin_amdgcn_sched_barrier(0);  // issued here, not sunk below the next reads
+                        } else if constexpr (V8RPM == 2 && qq == 1) {
+                            i32x2 &r0 = rv[(i - 1) % NB], &r1 = rv[i % NB];
+                            lgkm_wait2<ahead>(r0, r1);
+                            o[d] = T::mfma8(cat4(r0, r1, r0, r1), cat2(pk[0][0], x8{}), o[d]);
+                            __builtin_amdgcn_sched_barrier(0);
                         }
                         if constexpr (i + PF < NM) issue(std::integral_constant<int, i + PF>());
                     });
@@ -1040,17 +1074,18 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
                     for (int d = 0; d < DT; ++d)
 #pragma unroll
-                        for (int kk = 0; kk < NKT / 2; ++kk)
+                        for (int kk = 0; kk < (NKT + 1) / 2; ++kk)
                             if (2 * kk < nkt_act) {
                                 i32x2 r[4];
 #pragma unroll
                                 for (int qq = 0; qq < 4; ++qq) {
                                     r[qq] = (i32x2){0, 0};
-                                    if (2 * kk + qq / 2 < nkt_act)
+                                    if (2 * kk + qq / 2 < nkt_act && 2 * kk + qq / 2 < NKT)
                                         r[qq] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                                            (RSFA_LDS i32x2*)(vt_lds + (4 * kk + qq) * 16 * D + vo8[d]));
+                                            (RSFA_LDS i32x2*)(vt_lds + (4 * kk + qq) * 16 * D + v8_off(d)));
                                 }
-                                o[d] = T::mfma8(cat4(r[0], r[1], r[2], r[3]), cat2(pk[2 * kk][0], pk[2 * kk + 1][0]), o[d]);
+                                o[d] = T::mfma8(cat4(r[0], r[1], r[2], r[3]),
+                                                cat2(pk[2 * kk][0], 2 * kk + 1 < NKT ? pk[(2 * kk + 1) % NKT][0] : x8{}), o[d]);
                             }
                 }
             } else if (!MASK) {
@@ -1152,18 +1187,21 @@ fa_fwd_kernel(FwdParams p) {
                 // V8: rlo only, read PFV ahead (two float8 MFMAs; one is
                 // shorter than an LDS read's latency), and the four reads of
                 // a float8 MFMA stay live to it
-                constexpr int PFV = V8 ? 8 : XPF;
-                constexpr int XNBV = V8 ? PFV + 4 : XNB;
+                constexpr int PFV = V8 ? (V8RPM == 2 ? 4 : 8) : XPF;
+                constexpr int XNBV = V8 ? PFV + V8RPM : XNB;
                 i32x2 rlo[XNBV], rhi[XNB];
                 i32x4 kr[XNB];
                 uint32_t xa[4];  // V reads (two halves), K reads (even / odd k-steps)
-                uint32_t xv[V8 ? DT : 1];  // V8: V reads per head-dim block
+                uint32_t xv[V8 && !V8_INLINE ? DT : 1];  // V8: V reads per head-dim block (V8_INLINE: the tile)
                 auto x_issue = [&](auto mc) {
                     constexpr int m = decltype(mc)::value;
                     if constexpr (m < NPV) {
                         constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
                         if constexpr (V8) {
-                            rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[d]);
+                            if constexpr (V8_INLINE)
+                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[0] + v8_off(d));
+                            else
+                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[d]);
                         } else {
                             constexpr int off = (2 * kt + h2) * BLK + d * 1024;
                             rlo[m % XNB] = lds_read_tr16<off>(xa[0]);
@@ -1193,7 +1231,7 @@ fa_fwd_kernel(FwdParams p) {
                     static_assert(D0 >= 0 && D0 + NDMA * DSTEP <= M, "operand stream shorter than its loads");
                     if constexpr (V8) {
 #pragma unroll
-                        for (int d = 0; d < DT; ++d) xv[d] = b_tv + TILE + vo8[d];
+                        for (int d = 0; d < (V8_INLINE ? 1 : DT); ++d) xv[d] = b_tv + TILE + (V8_INLINE ? 0u : vo8[d]);
                     } else {
                         xa[0] = b_tv + TILE + voff[0];
                         xa[1] = b_tv + TILE + voff[1];
@@ -1214,7 +1252,13 @@ fa_fwd_kernel(FwdParams p) {
                                 // a 64-key float8 MFMA (as in pv_part), which
                                 // waits for its four reads
                                 constexpr int d = m / (2 * NKT), qq = m % (2 * NKT);
-                                if constexpr (qq % 4 == 3) {
+                                if constexpr (V8RPM == 2 && qq == 1) {
+                                    // a 32-key tile: the MFMA's upper 32 keys have P = 0
+                                    i32x2 &r0 = rlo[(m - 1) % XNBV], &r1 = rlo[m % XNBV];
+                                    lgkm_wait2<N>(r0, r1);
+                                    o[d] = T::mfma8(cat4(r0, r1, r0, r1), cat2(pk[0][0], x8{}), o[d]);
+                                    __builtin_amdgcn_sched_barrier(0);
+                                } else if constexpr (V8RPM == 4 && qq % 4 == 3) {
                                     i32x2 &r0 = rlo[(m - 3) % XNBV], &r1 = rlo[(m - 2) % XNBV], &r2 = rlo[(m - 1) % XNBV],
                                           &r3 = rlo[m % XNBV];
                                     lgkm_wait4<N>(r0, r1, r2, r3);

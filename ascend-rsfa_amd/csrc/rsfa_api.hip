@@ -429,9 +429,9 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     return RSFA_OK;
 }
 
-// Whether a float8 V is read as bytes by the kernels (head dims 64 and 128)
-// rather than from an fp16 copy.
-static bool v8_native(int64_t head_dim) { return head_dim == 64 || head_dim == 128; }
+// Whether a float8 V is read as bytes by the kernels (head dims 64, 128 and
+// 256) rather than from an fp16 copy.
+static bool v8_native(int64_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 
 uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim) {
     if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim) || v8_native(head_dim)) return 0;
@@ -488,8 +488,8 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // launch could pick (before any device work): the K/V loader's per-lane
     // 32-bit offsets, and the split state's 32-bit rows (task * BLOCK_M + row
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
-    // a float8 V is read from its fp16 copy, except at head dims 64 and 128
-    // (bytes, whose offsets are half those of the fp16 check)
+    // a float8 V is read from its fp16 copy, except at head dims 64, 128 and
+    // 256 (bytes, whose offsets are half those of the fp16 check)
     const int64_t v_rows = v8 && !v8_native(a->head_dim) ? a->head_dim : a->v_stride[2];
     for_each_kernel([&](const KernelEntry& e) {
         const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS

@@ -19,8 +19,8 @@
  *   rsfa_v8_workspace_bytes   -> (no separate counterpart: the size of the
  *                                fp16 copy of a float8 V, for the fp8_v
  *                                branch of _attn_fwd_inner, 208-211; zero
- *                                at head dims 64 and 128, which read V's
- *                                bytes)
+ *                                at head dims 64, 128 and 256, which read
+ *                                V's bytes)
  *   rsfa_strerror             -> (no counterpart: the reference raises Python
  *                                exceptions; codes map to them in the wrapper)
  *
@@ -75,12 +75,11 @@ typedef enum rsfa_dtype {
                                     P is rounded to e5m2 for P.V and the row
                                     sums add the unrounded P, as the reference's
                                     fp8_v branch does (208-211, 217).  At head
-                                    dims 64 and 128 the kernels read V's bytes
-                                    and run P.V on the e5m2 MFMA (no
-                                    workspace); at the other head dims the
-                                    library first
-                                    widens V to fp16 (exactly) in `workspace`:
-                                    see rsfa_v8_workspace_bytes */
+                                    dims 64, 128 and 256 the kernels read V's
+                                    bytes and run P.V on the e5m2 MFMA (no
+                                    workspace); at head dims 16 and 32 the
+                                    library first widens V to fp16 (exactly)
+                                    in `workspace`: see rsfa_v8_workspace_bytes */
 } rsfa_dtype;
 
 /* flags (bit set) */
@@ -168,8 +167,8 @@ uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                     int64_t head_dim, int32_t block_m);
 
 /* Bytes of workspace a float8 V (RSFA_DTYPE_F16_V8E5M2) needs: the fp16 copy
- * of V, contiguous [Z, H, N_CTX, D], or 0 at head dims 64 and 128 (their
- * kernels read the float8 bytes).  Split mode adds its state after it, at
+ * of V, contiguous [Z, H, N_CTX, D], at head dims 16 and 32, or 0 at head
+ * dims 64, 128 and 256 (their kernels read the float8 bytes).  Split mode adds its state after it, at
  * this offset.
  * 0 for invalid sizes. */
 uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,

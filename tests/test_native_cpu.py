@@ -128,11 +128,12 @@ def test_split_workspace_bytes_matches_reference_state_shape():
 
 def test_v8_workspace_bytes_is_the_fp16_copy_of_v():
     lib = _native.lib()
-    # head dims 64 and 128 read the float8 bytes themselves: no copy
+    # head dims 64, 128 and 256 read the float8 bytes themselves: no copy
     assert lib.rsfa_v8_workspace_bytes(32, 8, 2048, 128) == 0
     assert lib.rsfa_v8_workspace_bytes(32, 8, 2048, 64) == 0
-    assert lib.rsfa_v8_workspace_bytes(32, 8, 2048, 256) == 32 * 8 * 2048 * 256 * 2
+    assert lib.rsfa_v8_workspace_bytes(32, 8, 2048, 256) == 0
     assert lib.rsfa_v8_workspace_bytes(1, 1, 17, 16) == 17 * 16 * 2
+    assert lib.rsfa_v8_workspace_bytes(2, 8, 1024, 32) == 2 * 8 * 1024 * 32 * 2
     assert lib.rsfa_v8_workspace_bytes(1, 1, 17, 48) == 0
     assert lib.rsfa_v8_workspace_bytes(0, 1, 17, 64) == 0
 

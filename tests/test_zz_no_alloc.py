@@ -164,13 +164,14 @@ def _cpu_args(n=8192, d=128, **over):
 def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     lib = _native.lib()
     limit = _native.NOALLOC_WORKSPACE_BYTES
-    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x4096x256 is exactly the limit
-    fits = _cpu_args(n=4096, d=256, dtype=_native.DTYPE_F16_V8E5M2)
-    assert lib.rsfa_v8_workspace_bytes(1, 8, 4096, 256) == limit
-    over = _cpu_args(n=4096, d=256, dtype=_native.DTYPE_F16_V8E5M2, z=2)
+    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x32768x32 is exactly the limit
+    fits = _cpu_args(n=32768, d=32, dtype=_native.DTYPE_F16_V8E5M2)
+    assert lib.rsfa_v8_workspace_bytes(1, 8, 32768, 32) == limit
+    over = _cpu_args(n=32768, d=32, dtype=_native.DTYPE_F16_V8E5M2, z=2)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(over), None) == _native.E_SCRATCH
-    # at head dims 64 and 128 the kernels read a float8 V's bytes: no copy, any size
+    # at head dims 64, 128 and 256 the kernels read a float8 V's bytes: no copy, any size
     assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 128) == 0
+    assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 256) == 0
     big_v8 = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
     # split state: (2 + head_dim) fp32 per query row, rounded to the tile
     split = _cpu_args(z=8, h=32, n_ctx=16384, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
