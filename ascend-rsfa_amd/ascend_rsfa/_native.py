@@ -35,6 +35,7 @@ FLAG_STATIC_SCHEDULE = 0x1
 FLAG_CAUSAL_SPLIT = 0x2
 FLAG_EXACT_TILE = 0x4
 FLAG_TILE_HINT = 0x8
+FLAG_SINGLE_BLOCKS = 0x10
 
 # rsfa_attention_fwd_noalloc's fixed workspace
 NOALLOC_WORKSPACE_BYTES = 16 << 20

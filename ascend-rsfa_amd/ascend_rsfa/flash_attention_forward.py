@@ -193,7 +193,7 @@ def _hint_mode(tile_hint, exact_tile):
 
 
 def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=False,
-            static_schedule=False, tile_hint=None, exact_tile=False, out=None):
+            static_schedule=False, single_blocks=False, tile_hint=None, exact_tile=False, out=None):
     """Run the forward kernel; returns ``o`` or ``(o, lse)``.
 
     ``BM``/``BN`` keep the reference's meaning and validity rules (ValueError
@@ -205,7 +205,10 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
     two-launch prefix/diagonal split, handing (m, l, acc) over in an fp32
     workspace;
     ``static_schedule=True`` replaces the dynamic task queue by the
-    reference's grid-stride order (results are bitwise identical).  ``lse`` is
+    reference's grid-stride order, and ``single_blocks=True`` makes every
+    causal task one query block instead of the pairs of blocks (nmb-1-i, i)
+    the library otherwise uses when they fill whole rounds of the grid (results
+    are bitwise identical either way).  ``lse`` is
     the natural-log logsumexp of the scaled scores, fp32 [Z, H, N].
     """
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -254,7 +257,8 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
         args.block_m = bm
         args.block_n = bn
         args.flags = _native.FLAG_EXACT_TILE | (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
-            _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0)
+            _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0) | (
+            _native.FLAG_SINGLE_BLOCKS if single_blocks else 0)
         # workspace: the fp16 copy of a float8 V, then the split state
         nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0
         if split and causal:

@@ -170,6 +170,7 @@ struct FwdParams {
     int32_t num_heads;  // Z * H
     int32_t num_tasks;  // num_heads * nmb
     int32_t nq;         // task queues (1 or 8): queue x holds the heads bh % nq == x
+    int32_t pairs;      // causal, fused mode: a ticket runs query blocks nmb-1-i and i
     float c;            // |sm_scale| * log2(e)
     uint32_t neg;       // 1 when sm_scale < 0: q is negated (exact) and c = |c|
     uint32_t* ticket;   // dynamic queue counters (nq of them, 16 words apart; each returns
@@ -181,25 +182,40 @@ struct FwdParams {
 // query blocks of a head run on one XCD and its K/V are fetched into that
 // XCD's L2 once, instead of once per XCD.
 struct Queue {
-    int x;      // queue index
-    int nh;     // heads in the queue
-    int ntask;  // tasks in the queue = nh * nmb
-    int nwg;    // workgroups serving the queue
-    int rank;   // this workgroup's rank among them
-    int tail;   // causal: heads at the queue's end served heavy-first across heads
+    int x;        // queue index
+    int nh;       // heads in the queue
+    int ntask;    // task indices of the queue: nh * nmb, or 2 * nticket with pairs
+    int nticket;  // tickets of the queue: nh * nmb, or nh * pph with pairs
+    int nwg;      // workgroups serving the queue
+    int rank;     // this workgroup's rank among them
+    int tail;     // causal: heads at the queue's end served heavy-first across heads
+    int pph;      // causal pairs per head (0: no pairs): ticket k runs tasks 2k, 2k+1
+    int odd;      // nmb is odd: a head's last pair holds the middle query block alone
 };
 
-template <bool CAUSAL>
+template <bool PAIRS>
 __device__ __forceinline__ Queue make_queue(const FwdParams& p) {
     Queue q;
     q.x = (int)blockIdx.x % p.nq;
     q.rank = (int)blockIdx.x / p.nq;
     q.nwg = ((int)gridDim.x - q.x + p.nq - 1) / p.nq;
     q.nh = (p.num_heads - q.x + p.nq - 1) / p.nq;
-    q.ntask = q.nh * p.nmb;
+    q.pph = PAIRS && p.pairs ? (p.nmb + 1) / 2 : 0;
+    q.odd = p.nmb & 1;
+    q.nticket = q.pph ? q.nh * q.pph : q.nh * p.nmb;
+    q.ntask = q.pph ? 2 * q.nticket : q.nticket;
     // the tail spans about two rounds of the queue's workgroups
-    q.tail = CAUSAL ? max(1, min(q.nh, 2 * (q.nwg / p.nmb))) : 0;
+    q.tail = max(1, min(q.nh, 2 * (q.nwg / p.nmb)));
     return q;
+}
+
+// Pairs: the first task of ticket k is 2k; the second, 2k + 1, follows
+// without a ticket unless the pair is a head's middle block alone.
+__device__ __forceinline__ int task_of_ticket(const Queue& q, int k) { return q.pph ? 2 * k : k; }
+__device__ __forceinline__ int ticket_of_task(const Queue& q, int t) { return q.pph ? t >> 1 : t; }
+__device__ __forceinline__ bool pair_continues(const Queue& q, int t) {
+    if (!q.pph || (t & 1)) return false;
+    return !(q.odd && (t >> 1) % q.pph == q.pph - 1);
 }
 
 __device__ __forceinline__ float swap_max(float x) {
@@ -216,18 +232,32 @@ __device__ __forceinline__ float swap_sum(float x) {
 // Task order inside a queue.  Head-major, so the tasks of a head start close
 // together in time and walk its K/V in the same order: the first fetches a
 // key tile into the XCD's L2 and the others hit it (causal tasks of one head
-// all start at key tile 0).  Causal: inside a head the heaviest query block
-// first, and the last q.tail heads are served heavy-first across heads
-// (longest-processing-time first), which bounds the persistent grid's tail.
-// Grouping heads heavy-first over the whole queue balances as well but
-// spreads a head's tasks over several rounds of tickets, and their K/V are
-// evicted between them (measured at B=128 H=8 S=2048 D=128 causal: 2.09x the
-// Q+K+V bytes fetched past L2, against 1.84x head-major; 4 % slower at
-// B=4 H=16 S=8192 D=64 and 10 % at B=16 H=8 S=1024).
+// all start at key tile 0).
+// Causal with pairs (the host's choice when the pairs fill whole rounds of
+// the queue's workgroups): ticket k of a head runs its query block nmb-1-i,
+// then block i, so every ticket carries nmb + 1 block-lengths of key tiles.
+// The workgroups then run in lockstep rounds, as in the non-causal case, and
+// a head's heavy halves walk its K/V together (key tiles fetched past L2 at
+// B=128 H=8 S=2048 D=128: 1.42x Q+K+V against 1.88x single blocks; at
+// B=4 H=16 S=8192 D=64 1.21x against 1.87x, 3 % faster).  Light block first
+// instead: 2.26x and 1.00x.
+// Causal single blocks: inside a head the heaviest query block first, and the
+// last q.tail heads are served heavy-first across heads (longest-processing-
+// time first), which bounds the persistent grid's tail.  Grouping heads
+// heavy-first over the whole queue balances as well but spreads a head's
+// tasks over several rounds of tickets, and their K/V are evicted between
+// them (B=128 H=8 S=2048 D=128: 2.09x the Q+K+V bytes fetched past L2,
+// against 1.84x head-major; 4 % slower at B=4 H=16 S=8192 D=64 and 10 % at
+// B=16 H=8 S=1024).
 template <bool CAUSAL>
 __device__ __forceinline__ void decode_task(const FwdParams& p, const Queue& q, int t, int& bh, int& mb) {
     int lh;  // head index inside the queue
-    if (!CAUSAL) {
+    if (q.pph) {
+        const int k = t >> 1;
+        lh = k / q.pph;
+        const int i = k - lh * q.pph;
+        mb = (t & 1) ? i : p.nmb - 1 - i;
+    } else if (!CAUSAL) {
         lh = t / p.nmb;
         mb = t - lh * p.nmb;
     } else {
@@ -509,6 +539,13 @@ fa_fwd_kernel(FwdParams p) {
     // D = 256 shapes); the lane id is then taken from asm (v_mbcnt), which
     // the compiler cannot hoist.
     constexpr bool REG_TIGHT = D > 128;
+    // QREG (REG_TIGHT ping-pong kernels, whose Q does not fit a Q buffer):
+    // a task loads the next task's Q into the Q^T registers once its own
+    // last S^T product is issued, so the loads' latency passes during its
+    // last softmax, its last P.V and its epilogue instead of at the next
+    // task's start.
+    // (Not with a float8 V, whose D = 256 kernels spill more with it.)
+    constexpr bool QREG = REG_TIGHT && PP && MODE == MODE_FUSED && !QPF && !V8;
     auto fresh_lane = []() {
         int ln;
         asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
@@ -608,22 +645,28 @@ fa_fwd_kernel(FwdParams p) {
     const velem* const vgp = (const velem*)p.v;
     elem* const og = (elem*)p.o;
 
-    const Queue qu = make_queue<CAUSAL>(p);
+    constexpr bool PAIRS = CAUSAL && MODE == MODE_FUSED;
+    const Queue qu = make_queue<PAIRS>(p);
     uint32_t* const ctr = p.ticket ? p.ticket + 16 * qu.x : nullptr;
     int t;
     if (ctr) {
         if (tid == 0) *tslot = (int)atomicAdd(ctr, 1u);
         __syncthreads();
-        t = *tslot;
+        t = task_of_ticket(qu, *tslot);
         if constexpr (QPF) __syncthreads();  // read before the first task writes the slot again
     } else {
-        t = qu.rank;
+        t = task_of_ticket(qu, qu.rank);
     }
-    bool qready = false;  // QPF: the previous task loaded this task's Q into the Q buffer
+    bool qready = false;  // QPF / QREG: the previous task loaded this task's Q
+    // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7];
+    // QREG carries them from one task to the next
+    x8 qf[KST];
 
     while (t < qu.ntask) {
+        const int tcur = t;
         int nxt = 0;
-        if (ctr && tid == 0) {
+        const bool cont = pair_continues(qu, t);  // the next task needs no ticket
+        if (ctr && tid == 0 && !cont) {
             if constexpr (QPF) {
                 // from asm, so the compiler adds no wait for it before its use
                 // (the ticket slot write after the first phase's partial load
@@ -774,8 +817,9 @@ fa_fwd_kernel(FwdParams p) {
         // of a whole query block (q_dma, read after the first phase's load
         // wait), else global memory.
         const bool q_dma = QPF && !qready && jpp > j0 && m0 + BM <= n;
-        int t_next = -1;         // QPF, ticket queue: the next ticket, read at the first barrier
+        int t_next = -1;         // QPF, ticket queue / QREG: the next task, read in the ping-pong part
         bool qpf_do = false;     // QPF: this task loads the next task's Q into the Q buffer
+        bool qreg_do = false;    // QREG: this task loads the next task's Q into qf
         const elem* qnext = qg;  // its first row
         if (jpp > j0) {
             load_k(j0);
@@ -796,9 +840,7 @@ fa_fwd_kernel(FwdParams p) {
                 return qb + (int64_t)min(qrow, n - 1) * p.q_sm + hh * 8;
             }
         };
-        // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
-        // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
-        x8 qf[KST];
+        // sign flip of Q for a negative sm_scale: xor with a uniform mask, 0 otherwise
         auto q_sign = [&]() {
             int qs = qsign;
             // REG_TIGHT: tested here, in an SGPR (hoisted out of the task loop,
@@ -832,6 +874,12 @@ fa_fwd_kernel(FwdParams p) {
         };
         if (QPF && qready) {
             read_q();
+        } else if (QREG && qready) {
+            // loaded at the end of the previous task; waited for here, where
+            // the first tile's loads are in flight
+#pragma unroll
+            for (int s = 0; s < KST; ++s) asm volatile("" : "+v"(qf[s]));
+            q_sign();
         } else if (!q_dma) {
             const elem* const ql = q_lane();
 #pragma unroll
@@ -1328,7 +1376,9 @@ fa_fwd_kernel(FwdParams p) {
                     // the next task; when this task has at least four ping-pong
                     // tiles and the next one a whole query block, its Q is loaded
                     // in the phases X_{j0+2} and X_{j0+3}
-                    const int tn = ctr ? __builtin_amdgcn_readfirstlane(*tslot) : t + qu.nwg;
+                    const int tn = cont ? t + 1
+                                   : task_of_ticket(qu, ctr ? __builtin_amdgcn_readfirstlane(*tslot)
+                                                            : ticket_of_task(qu, t) + qu.nwg);
                     if (ctr) t_next = tn;
                     if (tn < qu.ntask && jpp - j0 >= 4) {
                         int nbh, nmb;
@@ -1345,6 +1395,13 @@ fa_fwd_kernel(FwdParams p) {
                 f32x16 sacc[NKT];
                 qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free, std::true_type());
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V_j0, K_j0+1, published by the next barrier
+                if constexpr (QREG) {
+                    // the next ticket (its atomic, older than the wait above, is
+                    // done), published by the next barrier: every wave reads it
+                    // after the last tile's softmax barrier
+                    if (ctr && tid == 0 && !cont) *tslot = nxt;
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                }
                 if (j0 + 2 < jpp) load_k(j0 + 2);
                 if (j0 + 1 < jpp) load_v(j0 + 1);
                 int t = j0;
@@ -1446,6 +1503,27 @@ fa_fwd_kernel(FwdParams p) {
                 {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
+                    if constexpr (QREG) {
+                        // every S^T product of the task is issued: the next
+                        // task's Q goes into qf now, unless key tiles past
+                        // the ping-pong loop still need this task's Q
+                        const int tn = cont ? tcur + 1
+                                       : task_of_ticket(qu, ctr ? __builtin_amdgcn_readfirstlane(*tslot)
+                                                                : ticket_of_task(qu, tcur) + qu.nwg);
+                        t_next = tn;
+                        if (tn < qu.ntask && jpp == j1) {
+                            int nbh, nmb;
+                            decode_task<CAUSAL>(p, qu, tn, nbh, nmb);
+                            const int nb = nbh / p.H, nh = nbh - nb * p.H;
+                            const int ln = fresh_lane();
+                            const elem* const ql = qg + nb * p.q_sz + nh * p.q_sh +
+                                                   (int64_t)min(nmb * BM + wave * 32 + (ln & 31), n - 1) * p.q_sm +
+                                                   ((ln >> 5) & 1) * 8;
+#pragma unroll
+                            for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(ql + 16 * s);
+                            qreg_do = true;
+                        }
+                    }
                     x8 pk[NKT][2];
                     if constexpr (DIAG_VM) vmask(sacc, t);
                     if constexpr (DIAG_PP) {
@@ -1582,26 +1660,28 @@ fa_fwd_kernel(FwdParams p) {
 
         if (ctr) {
             __syncthreads();
-            if (QPF && t_next >= 0) {
+            if ((QPF || QREG) && t_next >= 0) {
                 t = t_next;
+            } else if (cont) {
+                t = t + 1;
             } else {
                 if (tid == 0) *tslot = nxt;
                 __syncthreads();
-                t = *tslot;
+                t = task_of_ticket(qu, *tslot);
                 if constexpr (QPF) __syncthreads();  // read before the next task writes the slot
             }
         } else {
             __syncthreads();
-            t += qu.nwg;
+            t = cont ? t + 1 : task_of_ticket(qu, ticket_of_task(qu, t) + qu.nwg);
         }
-        qready = qpf_do;
+        qready = qpf_do || qreg_do;
     }
 
     // The workgroup holding the last ticket handed out by its queue returns the
     // counter to zero for the next launch on this stream: every workgroup of
     // the queue draws exactly one ticket >= ntask, so that ticket is
     // ntask + nwg - 1.
-    if (ctr && tid == 0 && t == qu.ntask + qu.nwg - 1) atomicExch(ctr, 0u);
+    if (ctr && tid == 0 && ticket_of_task(qu, t) == qu.nticket + qu.nwg - 1) atomicExch(ctr, 0u);
 }
 
 }  // namespace rsfa

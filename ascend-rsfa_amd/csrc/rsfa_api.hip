@@ -152,6 +152,32 @@ int32_t queue_count(int64_t num_heads, int64_t grid) {
     return kQueues;
 }
 
+// Whether a causal fused launch hands out its query blocks in pairs (nmb-1-i,
+// then i, as one ticket: every ticket the same length, nmb + 1 block-lengths
+// of key tiles).  Pairs run in lockstep rounds and fetch fewer K/V bytes past
+// L2, but a last round that the pairs fill only partly idles workgroups for a
+// whole pair, where single blocks served longest-first end closer together.
+// Makespans per queue in block-lengths, with Wq workgroups: pairs
+// ceil(heads * nmb / 2 / Wq) * (nmb + 1), single blocks about their total
+// work / Wq + 1/2; pairs win ties within 3 %.  Only for kernels that load the
+// next task's Q during the current one (`qbuf`): the others load Q at a
+// task's start, and in lockstep rounds every workgroup of the grid does so at
+// once (measured at D = 256: 0.5-0.8 % slower with pairs).  Only for an even
+// nmb, whose pairs are all whole (B=64 H=8 S=1792 D=128: 1.5 % slower with
+// the middle blocks alone).
+int32_t use_pairs(int64_t num_heads, int32_t nmb, int64_t grid, int32_t nq, bool qbuf) {
+    if (!qbuf || nmb < 2 || (nmb & 1)) return 0;
+    const int64_t wq = grid / nq;                  // workgroups per queue
+    const int64_t hq = (num_heads + nq - 1) / nq;  // heads of the fullest queue
+    if (wq < 1) return 0;
+    const double rounds = (double)hq * nmb / 2.0 / (double)wq;
+    if (rounds < 1.0) return 0;
+    const double len = nmb + 1.0;
+    const double paired = std::ceil(rounds - 1e-9) * len;
+    const double single = rounds * len + 0.5;
+    return paired <= 1.03 * single ? 1 : 0;
+}
+
 // Position of an instantiation in the kernel lists (a fixed-size cache index).
 int kernel_index(const KernelEntry& e) {
     int base = 0;
@@ -586,6 +612,10 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
         grid = std::min<int64_t>(grid, p.num_tasks);
         grid = std::max<int64_t>(grid, 1);
         p.nq = queue_count(p.num_heads, grid);
+        p.pairs = causal && modes[li] == MODE_FUSED && !(a->flags & RSFA_FLAG_SINGLE_BLOCKS)
+                      ? use_pairs(p.num_heads, p.nmb, grid, p.nq,
+                                  uses_q_buffer(k->d, k->bn, k->nw, true, MODE_FUSED))
+                      : 0;
         p.ticket = !dynamic ? nullptr : tickets_given ? tickets : stream_ticket(ds, stream);
         void* args[] = {&p};
         if (hipLaunchKernel(k->fn, dim3((unsigned)grid), dim3((unsigned)(k->nw * 64)), args, 0,

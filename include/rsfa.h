@@ -97,6 +97,11 @@ typedef enum rsfa_dtype {
 #define RSFA_FLAG_TILE_HINT       0x8u /* a valid request is only checked, and
                                           the tile rsfa_get_tiling picks for
                                           the shape runs                        */
+#define RSFA_FLAG_SINGLE_BLOCKS   0x10u /* causal: one query block per task
+                                          instead of the pairs (nmb-1-i, i) the
+                                          library uses when they fill whole
+                                          rounds of the grid; same results,
+                                          bit for bit (a scheduling knob)       */
 
 typedef struct rsfa_fwd_args {
     uint32_t    struct_size;  /* = sizeof(rsfa_fwd_args)                        */

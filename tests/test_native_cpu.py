@@ -223,3 +223,12 @@ def test_attention_fwd_limits_admit_the_boundary(over):
         pytest.skip("a GPU is visible; this check needs a machine without one")
     lib = _native.lib()
     assert lib.rsfa_attention_fwd(ctypes.byref(_valid_args(**over)), None) == _native.E_DEVICE
+
+
+def test_flag_constants_match_the_header():
+    """The wrapper's flag bits are the header's RSFA_FLAG_* values."""
+    hdr = open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include", "rsfa.h")).read()
+    flags = {m.group(1): int(m.group(2), 16) for m in re.finditer(r"#define RSFA_FLAG_(\w+)\s+(0x[0-9a-fA-F]+)u", hdr)}
+    assert flags == {"STATIC_SCHEDULE": 1, "CAUSAL_SPLIT": 2, "EXACT_TILE": 4, "TILE_HINT": 8, "SINGLE_BLOCKS": 16}
+    for name, val in flags.items():
+        assert getattr(_native, "FLAG_" + name) == val

@@ -328,6 +328,45 @@ def test_dynamic_and_static_schedules_bitwise_equal(causal):
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
+# Causal shapes whose query blocks the library hands out in pairs (nmb-1-i,
+# then i, per ticket) on a 256-CU MI355X: head dims 64 and 128 (the Q-buffer
+# kernels), an even nmb, and pairs that fill whole rounds of the 32 workgroups
+# of each of the 8 queues (heads per queue * nmb / 2 a multiple of 32).  A
+# partial last block, bf16, and pairs over several rounds.
+PAIR_SHAPES = [
+    (16, 8, 1024, 128, torch.float16),
+    (16, 8, 1900, 128, torch.float16),
+    (8, 8, 2048, 64, torch.float16),
+    (16, 8, 1024, 128, torch.bfloat16),
+    (32, 8, 2048, 128, torch.float16),
+]
+
+
+@pytest.mark.parametrize("Z,H,N,D,dtype", PAIR_SHAPES)
+def test_causal_pairs_match_single_blocks_bitwise(Z, H, N, D, dtype):
+    """Pairs change only which workgroup runs a query block and when: the
+    output is bitwise that of one block per task (RSFA_FLAG_SINGLE_BLOCKS),
+    under the dynamic queue and the static order alike, and a second launch
+    (the queue counter reset by the first) repeats it.  Every head against
+    the fp32 closed form on the GPU, sampled heads against the CPU oracle."""
+    q, k, v = A.make_inputs(Z, H, N, D, seed=N + D, dtype=dtype)
+    qd, kd, vd = _to_gpu(q, k, v)
+    scale = 1 / math.sqrt(D)
+    a = F.forward(qd, kd, vd, True, scale)
+    b = F.forward(qd, kd, vd, True, scale, single_blocks=True)
+    c = F.forward(qd, kd, vd, True, scale, static_schedule=True)
+    d = F.forward(qd, kd, vd, True, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "pairs and single blocks differ"
+    assert torch.equal(a, c) and torch.equal(a, d), "pair schedules differ"
+    ref = _gpu_reference(qd, kd, vd, True, scale)
+    assert torch.allclose(a.float(), ref, atol=ATOL, rtol=RTOL), (a.float() - ref).abs().max().item()
+    for (zi, hi) in _sample_heads(Z, H, 2, seed=N):
+        oref = A.reference_attention(q[zi:zi + 1, hi:hi + 1], k[zi:zi + 1, hi:hi + 1], v[zi:zi + 1, hi:hi + 1],
+                                     True, scale)
+        _assert_close(a[zi:zi + 1, hi:hi + 1], oref, f"pairs {Z}x{H}x{N}x{D} head ({zi},{hi})")
+
+
 @pytest.mark.parametrize("BM,BN", [(128, 64), (128, 128), (64, 64)])
 def test_causal_two_launch_split_matches_fused(BM, BN):
     q, k, v = A.make_inputs(2, 4, 1024, 64, seed=16)
