@@ -539,13 +539,6 @@ fa_fwd_kernel(FwdParams p) {
     // D = 256 shapes); the lane id is then taken from asm (v_mbcnt), which
     // the compiler cannot hoist.
     constexpr bool REG_TIGHT = D > 128;
-    // QREG (REG_TIGHT ping-pong kernels, whose Q does not fit a Q buffer):
-    // a task loads the next task's Q into the Q^T registers once its own
-    // last S^T product is issued, so the loads' latency passes during its
-    // last softmax, its last P.V and its epilogue instead of at the next
-    // task's start.
-    // (Not with a float8 V, whose D = 256 kernels spill more with it.)
-    constexpr bool QREG = REG_TIGHT && PP && MODE == MODE_FUSED && !QPF && !V8;
     auto fresh_lane = []() {
         int ln;
         asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
@@ -657,13 +650,9 @@ fa_fwd_kernel(FwdParams p) {
     } else {
         t = task_of_ticket(qu, qu.rank);
     }
-    bool qready = false;  // QPF / QREG: the previous task loaded this task's Q
-    // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7];
-    // QREG carries them from one task to the next
-    x8 qf[KST];
+    bool qready = false;  // QPF: the previous task loaded this task's Q into the Q buffer
 
     while (t < qu.ntask) {
-        const int tcur = t;
         int nxt = 0;
         const bool cont = pair_continues(qu, t);  // the next task needs no ticket
         if (ctr && tid == 0 && !cont) {
@@ -817,9 +806,8 @@ fa_fwd_kernel(FwdParams p) {
         // of a whole query block (q_dma, read after the first phase's load
         // wait), else global memory.
         const bool q_dma = QPF && !qready && jpp > j0 && m0 + BM <= n;
-        int t_next = -1;         // QPF, ticket queue / QREG: the next task, read in the ping-pong part
+        int t_next = -1;         // QPF, ticket queue: the next ticket, read at the first barrier
         bool qpf_do = false;     // QPF: this task loads the next task's Q into the Q buffer
-        bool qreg_do = false;    // QREG: this task loads the next task's Q into qf
         const elem* qnext = qg;  // its first row
         if (jpp > j0) {
             load_k(j0);
@@ -840,7 +828,9 @@ fa_fwd_kernel(FwdParams p) {
                 return qb + (int64_t)min(qrow, n - 1) * p.q_sm + hh * 8;
             }
         };
-        // sign flip of Q for a negative sm_scale: xor with a uniform mask, 0 otherwise
+        // Q^T fragments (B operand of S^T): lane holds q[qrow][16s + 8hh .. +7]
+        // (sign flip for a negative sm_scale: xor with a uniform mask, 0 otherwise)
+        x8 qf[KST];
         auto q_sign = [&]() {
             int qs = qsign;
             // REG_TIGHT: tested here, in an SGPR (hoisted out of the task loop,
@@ -874,12 +864,6 @@ fa_fwd_kernel(FwdParams p) {
         };
         if (QPF && qready) {
             read_q();
-        } else if (QREG && qready) {
-            // loaded at the end of the previous task; waited for here, where
-            // the first tile's loads are in flight
-#pragma unroll
-            for (int s = 0; s < KST; ++s) asm volatile("" : "+v"(qf[s]));
-            q_sign();
         } else if (!q_dma) {
             const elem* const ql = q_lane();
 #pragma unroll
@@ -1395,13 +1379,6 @@ fa_fwd_kernel(FwdParams p) {
                 f32x16 sacc[NKT];
                 qk_part(bofs(j0), j0 * BN, NKT, sacc, mask_free, std::true_type());
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V_j0, K_j0+1, published by the next barrier
-                if constexpr (QREG) {
-                    // the next ticket (its atomic, older than the wait above, is
-                    // done), published by the next barrier: every wave reads it
-                    // after the last tile's softmax barrier
-                    if (ctr && tid == 0 && !cont) *tslot = nxt;
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                }
                 if (j0 + 2 < jpp) load_k(j0 + 2);
                 if (j0 + 1 < jpp) load_v(j0 + 1);
                 int t = j0;
@@ -1503,27 +1480,6 @@ fa_fwd_kernel(FwdParams p) {
                 {
                     phase_barrier();  // Y of the last tile
                     prio_valu();
-                    if constexpr (QREG) {
-                        // every S^T product of the task is issued: the next
-                        // task's Q goes into qf now, unless key tiles past
-                        // the ping-pong loop still need this task's Q
-                        const int tn = cont ? tcur + 1
-                                       : task_of_ticket(qu, ctr ? __builtin_amdgcn_readfirstlane(*tslot)
-                                                                : ticket_of_task(qu, tcur) + qu.nwg);
-                        t_next = tn;
-                        if (tn < qu.ntask && jpp == j1) {
-                            int nbh, nmb;
-                            decode_task<CAUSAL>(p, qu, tn, nbh, nmb);
-                            const int nb = nbh / p.H, nh = nbh - nb * p.H;
-                            const int ln = fresh_lane();
-                            const elem* const ql = qg + nb * p.q_sz + nh * p.q_sh +
-                                                   (int64_t)min(nmb * BM + wave * 32 + (ln & 31), n - 1) * p.q_sm +
-                                                   ((ln >> 5) & 1) * 8;
-#pragma unroll
-                            for (int s = 0; s < KST; ++s) qf[s] = *(const x8*)(ql + 16 * s);
-                            qreg_do = true;
-                        }
-                    }
                     x8 pk[NKT][2];
                     if constexpr (DIAG_VM) vmask(sacc, t);
                     if constexpr (DIAG_PP) {
@@ -1660,7 +1616,7 @@ fa_fwd_kernel(FwdParams p) {
 
         if (ctr) {
             __syncthreads();
-            if ((QPF || QREG) && t_next >= 0) {
+            if (QPF && t_next >= 0) {
                 t = t_next;
             } else if (cont) {
                 t = t + 1;
@@ -1674,7 +1630,7 @@ fa_fwd_kernel(FwdParams p) {
             __syncthreads();
             t = cont ? t + 1 : task_of_ticket(qu, ticket_of_task(qu, t) + qu.nwg);
         }
-        qready = qpf_do || qreg_do;
+        qready = qpf_do;
     }
 
     // The workgroup holding the last ticket handed out by its queue returns the
