@@ -184,13 +184,11 @@ struct FwdParams {
 struct Queue {
     int x;        // queue index
     int nh;       // heads in the queue
-    int ntask;    // task indices of the queue: nh * nmb, or 2 * nticket with pairs
-    int nticket;  // tickets of the queue: nh * nmb, or nh * pph with pairs
+    int ntask;    // task indices of the queue: nh * nmb, or 2 * nh * pph with pairs
     int nwg;      // workgroups serving the queue
     int rank;     // this workgroup's rank among them
     int tail;     // causal: heads at the queue's end served heavy-first across heads
     int pph;      // causal pairs per head (0: no pairs): ticket k runs tasks 2k, 2k+1
-    int odd;      // nmb is odd: a head's last pair holds the middle query block alone
 };
 
 template <bool PAIRS>
@@ -201,9 +199,7 @@ __device__ __forceinline__ Queue make_queue(const FwdParams& p) {
     q.nwg = ((int)gridDim.x - q.x + p.nq - 1) / p.nq;
     q.nh = (p.num_heads - q.x + p.nq - 1) / p.nq;
     q.pph = PAIRS && p.pairs ? (p.nmb + 1) / 2 : 0;
-    q.odd = p.nmb & 1;
-    q.nticket = q.pph ? q.nh * q.pph : q.nh * p.nmb;
-    q.ntask = q.pph ? 2 * q.nticket : q.nticket;
+    q.ntask = q.pph ? 2 * q.nh * q.pph : q.nh * p.nmb;
     // the tail spans about two rounds of the queue's workgroups
     q.tail = max(1, min(q.nh, 2 * (q.nwg / p.nmb)));
     return q;
@@ -213,9 +209,9 @@ __device__ __forceinline__ Queue make_queue(const FwdParams& p) {
 // without a ticket unless the pair is a head's middle block alone.
 __device__ __forceinline__ int task_of_ticket(const Queue& q, int k) { return q.pph ? 2 * k : k; }
 __device__ __forceinline__ int ticket_of_task(const Queue& q, int t) { return q.pph ? t >> 1 : t; }
-__device__ __forceinline__ bool pair_continues(const Queue& q, int t) {
+__device__ __forceinline__ bool pair_continues(const FwdParams& p, const Queue& q, int t) {
     if (!q.pph || (t & 1)) return false;
-    return !(q.odd && (t >> 1) % q.pph == q.pph - 1);
+    return !((p.nmb & 1) && (t >> 1) % q.pph == q.pph - 1);
 }
 
 __device__ __forceinline__ float swap_max(float x) {
@@ -654,8 +650,10 @@ fa_fwd_kernel(FwdParams p) {
 
     while (t < qu.ntask) {
         int nxt = 0;
-        const bool cont = pair_continues(qu, t);  // the next task needs no ticket
-        if (ctr && tid == 0 && !cont) {
+        // the next task needs no ticket when it is the second of a pair
+        // (recomputed where needed: a flag kept live across the task costs a
+        // register of the tight causal kernels)
+        if (ctr && tid == 0 && !pair_continues(p, qu, t)) {
             if constexpr (QPF) {
                 // from asm, so the compiler adds no wait for it before its use
                 // (the ticket slot write after the first phase's partial load
@@ -1360,7 +1358,7 @@ fa_fwd_kernel(FwdParams p) {
                     // the next task; when this task has at least four ping-pong
                     // tiles and the next one a whole query block, its Q is loaded
                     // in the phases X_{j0+2} and X_{j0+3}
-                    const int tn = cont ? t + 1
+                    const int tn = pair_continues(p, qu, t) ? t + 1
                                    : task_of_ticket(qu, ctr ? __builtin_amdgcn_readfirstlane(*tslot)
                                                             : ticket_of_task(qu, t) + qu.nwg);
                     if (ctr) t_next = tn;
@@ -1618,7 +1616,7 @@ fa_fwd_kernel(FwdParams p) {
             __syncthreads();
             if (QPF && t_next >= 0) {
                 t = t_next;
-            } else if (cont) {
+            } else if (pair_continues(p, qu, t)) {
                 t = t + 1;
             } else {
                 if (tid == 0) *tslot = nxt;
@@ -1628,7 +1626,7 @@ fa_fwd_kernel(FwdParams p) {
             }
         } else {
             __syncthreads();
-            t = cont ? t + 1 : task_of_ticket(qu, ticket_of_task(qu, t) + qu.nwg);
+            t = pair_continues(p, qu, t) ? t + 1 : task_of_ticket(qu, ticket_of_task(qu, t) + qu.nwg);
         }
         qready = qpf_do;
     }
@@ -1637,7 +1635,7 @@ fa_fwd_kernel(FwdParams p) {
     // counter to zero for the next launch on this stream: every workgroup of
     // the queue draws exactly one ticket >= ntask, so that ticket is
     // ntask + nwg - 1.
-    if (ctr && tid == 0 && ticket_of_task(qu, t) == qu.nticket + qu.nwg - 1) atomicExch(ctr, 0u);
+    if (ctr && tid == 0 && ticket_of_task(qu, t) == ticket_of_task(qu, qu.ntask) + qu.nwg - 1) atomicExch(ctr, 0u);
 }
 
 }  // namespace rsfa
