@@ -19,10 +19,14 @@ config's inputs are drawn and made resident before the first timing, and each
 config then gets the same steady state: about ``--device-warmup-s`` seconds of
 back-to-back launches (an idle GPU drops its clocks, and the first launches
 after a pause run below the steady rate), ``--warmup`` untimed calls, then
-``--steps`` timed calls.
+``--windows`` back-to-back windows of exactly ``--steps`` timed calls, each
+between two HIP events with a device synchronisation before and after; the
+median window is reported (``windows_ms`` lists all), so that a transient
+in one window (a clock step of the board's power management; seen as one
+window 11 % slow among repeats) does not decide the figure.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
-                    [--calibrate-copy-mib M] [--device-warmup-s S]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--windows N] [--no-cpu]
+                    [--only NAME] [--calibrate-copy-mib M] [--device-warmup-s S]
 
 ``--calibrate-copy-mib M`` adds one plain device-to-device copy of M MiB after
 the timed work; under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives
@@ -145,7 +149,7 @@ def resident_inputs(torch, cfg, keep_cpu=False):
     return dev, fp_ok, ((q_c, k_c, v_c) if keep_cpu else None)
 
 
-def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0):
+def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0, windows=1):
     name, B, H, S, D, causal, scale, seed = cfg[:8]
     v8 = len(cfg) > 8 and cfg[8] == "e5m2"
     q, k, v = inputs
@@ -163,17 +167,21 @@ def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0
     stream = torch.cuda.current_stream()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for _ in range(steps):
-        F.attention(q, k, v, causal, scale, BM, BN)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    win = []
+    for _ in range(max(1, windows)):
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(steps):
+            F.attention(q, k, v, causal, scale, BM, BN)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        win.append(t0.elapsed_time(t1) / steps)
+    ms = sorted(win)[(len(win) - 1) // 2]  # the median window (the lower one of an even count)
     fl = flops(B, H, S, D, causal)
     res = {
         "B": B, "H": H, "S": S, "D": D, "causal": causal, "sm_scale": scale, "seed": seed, "tiling": [BM, BN],
-        "ms_per_call": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+        "ms_per_call": round(ms, 4), "windows_ms": [round(w, 4) for w in win],
+        "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
         "pct_peak": round(100.0 * fl / (ms * 1e-3) / 1e12 / peak_tflops(cfg), 2),
         **({"peak_tflops": peak_tflops(cfg)} if peak_tflops(cfg) != PEAK_TFLOPS else {}),
         "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal, 1 if v8 else 2) / (ms * 1e-3) / 1e9, 1),
@@ -288,6 +296,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default=None, help="time only this config name")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0)
+    ap.add_argument("--windows", type=int, default=3,
+                    help="windows of --steps timed calls per config; the median window is reported")
     ap.add_argument("--device-warmup-s", type=float, default=DEVICE_WARMUP_S,
                     help="seconds of back-to-back launches before each config (0 under counter passes)")
     args = ap.parse_args()
@@ -321,7 +331,7 @@ def main():
         key = FINGERPRINT_KEY.get(cfg[0], cfg[0]) + ("-" + cfg[8] if len(cfg) > 8 else "")
         dev, fp_ok = resident[key]
         results[cfg[0]] = time_config(F, torch, cfg, dev, fp_ok, args.steps, args.warmup,
-                                      device_warmup_s=args.device_warmup_s)
+                                      device_warmup_s=args.device_warmup_s, windows=args.windows)
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
     resident.clear()
     torch.cuda.empty_cache()
@@ -341,6 +351,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": r["ms_per_call"],
+        "timed_windows": args.windows,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -81,3 +81,29 @@ def test_roofline_bound_is_the_larger_floor():
     # a traffic figure names the committed profile it comes from
     if rt["traffic"] is not None:
         assert "not measured in this run" in rt["traffic_source"]
+
+
+def test_median_window_is_reported():
+    """time_config times --windows windows of exactly --steps calls and reports
+    the median one (a fake clock stands in for the HIP events)."""
+    import types
+    windows_ms = iter([12.0, 30.0, 10.0])  # elapsed ms of 3 windows of 10 steps
+
+    class Event:
+        def __init__(self, enable_timing=False):
+            pass
+
+        def record(self, stream=None):
+            pass
+
+        def elapsed_time(self, other):
+            return next(windows_ms)
+
+    calls = []
+    cuda = types.SimpleNamespace(Event=Event, synchronize=lambda: None, current_stream=lambda: None)
+    fake_torch = types.SimpleNamespace(cuda=cuda)
+    fake_F = types.SimpleNamespace(get_tiling=lambda *a: (256, 64), attention=lambda *a: calls.append(1))
+    cfg = bench.CONFIGS[0]
+    res = bench.time_config(fake_F, fake_torch, cfg, (None, None, None), True, steps=10, warmup=2, windows=3)
+    assert len(calls) == 2 + 3 * 10
+    assert res["windows_ms"] == [1.2, 3.0, 1.0] and res["ms_per_call"] == 1.2
