@@ -9,7 +9,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "librsfa.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # rsfa_status
 OK = 0

@@ -24,10 +24,8 @@ that are not on a GPU, the calls raise.
 
 A ``float8_e5m2`` V with float16 Q and K runs the reference's fp8_v branch
 (_attn_fwd_inner 208-211, 217): P is rounded to e5m2 for P.V while the row
-sums add the unrounded P; O is float16.  At head dims 64, 128 and 256 the
-kernels read V's bytes and run P.V on the e5m2 MFMA; at head dims 16 and 32
-the library first widens V to fp16 in a workspace (exact: an e5m2 byte is the
-high byte of that fp16) and P is rounded to e5m2 and widened back.
+sums add the unrounded P; O is float16.  The kernels read V's bytes and run
+P.V on the e5m2 MFMA at every head dim (no workspace).
 
 ``BM``/``BN`` keep the reference's meaning (query rows per program, keys per
 inner tile) and its validity rules: they select the tile, and the compiled
@@ -259,7 +257,7 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
         args.flags = _native.FLAG_EXACT_TILE | (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
             _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0) | (
             _native.FLAG_SINGLE_BLOCKS if single_blocks else 0)
-        # workspace: the fp16 copy of a float8 V, then the split state
+        # workspace: a float8 V needs none (rsfa_v8_workspace_bytes is 0); the split state
         nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0
         if split and causal:
             nbytes += split_workspace_bytes(Z, H, N, D, bm)

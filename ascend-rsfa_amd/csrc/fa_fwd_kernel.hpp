@@ -69,7 +69,6 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 constexpr float RESCALE_SLACK = 15.0f;
 
 struct TypeF16 {
-    static constexpr bool p8 = false;  // P rounded to the input dtype
     static constexpr bool v8 = false;  // V tiles in LDS as float8 bytes
     typedef _Float16 elem;
     typedef _Float16 velem;  // element of V in global memory
@@ -93,7 +92,6 @@ struct TypeF16 {
 };
 
 struct TypeBF16 {
-    static constexpr bool p8 = false;
     static constexpr bool v8 = false;
     typedef __bf16 elem;
     typedef __bf16 velem;
@@ -118,26 +116,11 @@ struct TypeBF16 {
 
 // fp16 Q, K, O with a float8 e5m2 V (reference flash_attention_forward.py:
 // 208-211, 253-256, 453-456: when V is float8e5, P is cast to float8e5 for
-// P.V, while the row sum l adds the unrounded P, 217 and 466).  The launcher
-// widens V to fp16 (exact: an e5m2 byte is the high byte of the fp16 with the
-// same value) and this type rounds P to e5m2 and widens it back the same way,
-// so the fp16 MFMA forms exactly the products of the e5m2 operands.
-struct TypeF16P8 : TypeF16 {
-    static constexpr bool p8 = true;
-    static __device__ __forceinline__ x2 cvt2(float a, float b) {
-        // two e5m2 bytes (round to nearest even) in bits 0-15 ...
-        const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
-        // ... become the high bytes of two fp16
-        return __builtin_bit_cast(x2, ((w << 8) & 0xFF00u) | ((w << 16) & 0xFF000000u));
-    }
-};
-
-// TypeF16P8 without the fp16 copy of V (head dim 128): V's tiles go into LDS
-// as the e5m2 bytes themselves (half the bytes of the copy), P is rounded to
-// e5m2 bytes, and P.V runs on the float8 MFMA (e5m2 x e5m2, 64 keys per MFMA,
-// twice the fp16 rate).  Its products are exact in fp32, as the fp16 MFMA's
-// are on the widened operands, and it accumulates in fp32.
-struct TypeF16V8 : TypeF16P8 {
+// P.V, while the row sum l adds the unrounded P, 217 and 466).  V's tiles go
+// into LDS as the e5m2 bytes themselves, P is rounded to e5m2 bytes, and P.V
+// runs on the float8 MFMA (e5m2 x e5m2, 64 keys per MFMA, twice the fp16
+// rate); its products are exact in fp32, and it accumulates in fp32.
+struct TypeF16V8 : TypeF16 {
     static constexpr bool v8 = true;
     typedef uint8_t velem;
     static __device__ __forceinline__ f32x16 mfma8(i32x8 a, i32x8 b, f32x16 c) {
@@ -445,25 +428,29 @@ fa_fwd_kernel(FwdParams p) {
     constexpr int BLK = 32 * DP;          // bytes of a 16-row block
     constexpr int TILE = BN * DP * 2;     // bytes of one K (or fp16 V) tile
     constexpr int NINST = BN * CPR / 64;  // 1-KB direct loads per tile
-    // V8: V tiles of e5m2 bytes, BN rows of D bytes; the 1-KB slice s holds
-    // rows V8RPS*s.. whole, and row R keeps its 16-byte chunk c at column
-    // c ^ v8_swz(R), so the eight rows one transposing read of P.V gathers
-    // (below), and the sixteen (row, chunk) pairs of 32 lanes, fall in
-    // distinct banks: R % 4 + 4 ((R / 8) % 2) for 128-byte rows (rows 2 apart
-    // share banks), 2 ((R / 8) % 2) for 64-byte rows (rows 4 apart do), and
-    // twice the 128-byte value for 256-byte rows (every row spans all banks,
-    // so the two chunk columns c, c ^ 1 one read takes from each of its eight
-    // rows must land on sixteen distinct columns).
+    // V8: V tiles of e5m2 bytes, BN rows of DP bytes (D = 16: the row's
+    // second 16-byte chunk is filler, its head dims are never stored); the
+    // 1-KB slice s holds rows V8RPS*s.. whole, and row R keeps its 16-byte
+    // chunk c at column c ^ v8_swz(R), so the eight rows one transposing read
+    // of P.V gathers (below), and the sixteen (row, chunk) pairs of 32 lanes,
+    // fall in distinct banks: R % 4 + 4 ((R / 8) % 2) for 128-byte rows (rows
+    // 2 apart share banks), 2 ((R / 8) % 2) for 64-byte rows (rows 4 apart
+    // do), and twice the 128-byte value for 256-byte rows (every row spans
+    // all banks, so the two chunk columns c, c ^ 1 one read takes from each of
+    // its eight rows must land on sixteen distinct columns).  32-byte rows
+    // keep their chunks in place (a chunk swap stays inside the row's banks).
     constexpr bool V8 = T::v8;
-    static_assert(!V8 || ((D == 64 || D == 128 || D == 256) && (BN % 64 == 0 || BN == 32)),
-                  "byte V tiles: head dim 64, 128 or 256; 64-key groups or one 32-key tile");
-    constexpr int TILEV = V8 ? BN * D : TILE;  // bytes of one V tile
+    static_assert(!V8 || (BN % 64 == 0 || BN == 32),
+                  "byte V tiles: 64-key groups or one 32-key tile");
+    constexpr int TILEV = V8 ? BN * DP : TILE;  // bytes of one V tile
     constexpr int BUF = TILE + TILEV;          // K + V
     constexpr int NINSTV = V8 ? TILEV / 1024 : NINST;
     constexpr int V8RPS = 1024 / DP;           // rows per 1-KB slice of a byte V tile
     constexpr int V8CPR = DP / 16;             // 16-byte chunks per row of it
     // (rq = R % 4, rh = (R / 8) % 2 of the row)
-    auto v8_swz = [](int rq, int rh) { return D == 64 ? 2 * rh : D == 128 ? rq + 4 * rh : 2 * (rq + 4 * rh); };
+    auto v8_swz = [](int rq, int rh) {
+        return D <= 32 ? 0 : D == 64 ? 2 * rh : D == 128 ? rq + 4 * rh : 2 * (rq + 4 * rh);
+    };
     // V8: transposing reads per float8 MFMA (64 keys): four, or two for a
     // 32-key tile, whose MFMA takes P = 0 for its upper 32 keys (and the same
     // two reads again as their finite V)
@@ -567,7 +554,7 @@ fa_fwd_kernel(FwdParams p) {
     int v8_rb = 0, v8_sw = 0;
     if constexpr (V8) {
         const int tr = l16 >> 1;  // row r of the group: R % 4 = r % 4, (R / 8) % 2 = r / 4
-        const int rowb = D * (4 * hh + (tr & 3) + 8 * (tr >> 2)) + 8 * (l16 & 1);
+        const int rowb = DP * (4 * hh + (tr & 3) + 8 * (tr >> 2)) + 8 * (l16 & 1);
         const int swz = v8_swz(tr & 3, tr >> 2);
         if constexpr (V8_INLINE) {
             v8_rb = rowb;
@@ -608,10 +595,11 @@ fa_fwd_kernel(FwdParams p) {
     }
     // V8: lane i of slice s fills position i of the slice, i.e. chunk column
     // i % V8CPR of row V8RPS*s + i / V8CPR, with that row's chunk
-    // (i % V8CPR) ^ v8_swz(row)
+    // (i % V8CPR) ^ v8_swz(row); at D = 16 the filler chunk re-reads chunk 0
+    // (a row has no second chunk to read)
     auto v8_chunk = [&](int s) {
         const int row = V8RPS * s + lane / V8CPR;
-        return (lane % V8CPR) ^ v8_swz(row & 3, (row >> 3) & 1);
+        return D < 32 ? 0 : (lane % V8CPR) ^ v8_swz(row & 3, (row >> 3) & 1);
     };
     if constexpr (V8) {
 #pragma unroll
@@ -1044,10 +1032,7 @@ fa_fwd_kernel(FwdParams p) {
                 l_sum += p0 + p1;  // the reference sums the unrounded P for an e5m2 V
             } else {
                 const x2 pr = T::cvt2(p0, p1);
-                if constexpr (T::p8)
-                    l_sum += p0 + p1;  // the reference sums the unrounded P for an e5m2 V
-                else
-                    l_sum = T::dot2(pr, T::ones2(), l_sum);
+                l_sum = T::dot2(pr, T::ones2(), l_sum);
                 pk[kt][h2][2 * i] = pr[0];
                 pk[kt][h2][2 * i + 1] = pr[1];
             }
@@ -1078,7 +1063,7 @@ fa_fwd_kernel(FwdParams p) {
                     auto issue = [&](auto ic) {
                         constexpr int i = decltype(ic)::value;
                         constexpr int d = i / (2 * NKT), kt = (i / 2) % NKT, h2 = i % 2;
-                        rv[i % NB] = lds_read_tr8<(2 * kt + h2) * 16 * D>(vb + v8_off(d));
+                        rv[i % NB] = lds_read_tr8<(2 * kt + h2) * 16 * DP>(vb + v8_off(d));
                     };
                     static_for<PF>(issue);
                     static_for<NM>([&](auto ic) {
@@ -1112,7 +1097,7 @@ fa_fwd_kernel(FwdParams p) {
                                     r[qq] = (i32x2){0, 0};
                                     if (2 * kk + qq / 2 < nkt_act && 2 * kk + qq / 2 < NKT)
                                         r[qq] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                                            (RSFA_LDS i32x2*)(vt_lds + (4 * kk + qq) * 16 * D + v8_off(d)));
+                                            (RSFA_LDS i32x2*)(vt_lds + (4 * kk + qq) * 16 * DP + v8_off(d)));
                                 }
                                 o[d] = T::mfma8(cat4(r[0], r[1], r[2], r[3]),
                                                 cat2(pk[2 * kk][0], 2 * kk + 1 < NKT ? pk[(2 * kk + 1) % NKT][0] : x8{}), o[d]);
@@ -1229,9 +1214,9 @@ fa_fwd_kernel(FwdParams p) {
                         constexpr int d = m / (2 * NKT), kt = (m / 2) % NKT, h2 = m % 2;
                         if constexpr (V8) {
                             if constexpr (V8_INLINE)
-                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[0] + v8_off(d));
+                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * DP>(xv[0] + v8_off(d));
                             else
-                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * D>(xv[d]);
+                                rlo[m % XNBV] = lds_read_tr8<(2 * kt + h2) * 16 * DP>(xv[d]);
                         } else {
                             constexpr int off = (2 * kt + h2) * BLK + d * 1024;
                             rlo[m % XNB] = lds_read_tr16<off>(xa[0]);

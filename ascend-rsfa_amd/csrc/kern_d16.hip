@@ -10,4 +10,4 @@ using namespace rsfa;
 #endif
 
 RSFA_DEFINE_KERNEL_LIST(kernels_d16, RSFA_D16_TILES(TypeF16, 0), RSFA_D16_TILES(TypeBF16, 1),
-                        RSFA_D16_TILES(TypeF16P8, 2))
+                        RSFA_D16_TILES(TypeF16V8, 2))

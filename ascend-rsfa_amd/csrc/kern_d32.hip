@@ -10,4 +10,4 @@ using namespace rsfa;
 #endif
 
 RSFA_DEFINE_KERNEL_LIST(kernels_d32, RSFA_D32_TILES(TypeF16, 0), RSFA_D32_TILES(TypeBF16, 1),
-                        RSFA_D32_TILES(TypeF16P8, 2))
+                        RSFA_D32_TILES(TypeF16V8, 2))

@@ -344,41 +344,11 @@ bool loader_offsets_fit(const KernelEntry& e, int64_t row_stride) {
     return ((int64_t)(e.bn - 1) * row_stride + dp) * 2 < (int64_t(1) << 32);
 }
 
-// Widens a float8 e5m2 V [Z, H, N, D] (strided, unit head-dim stride) into a
-// contiguous fp16 copy.  An e5m2 byte is the high byte of the fp16 of the same
-// value (same sign, exponent bias 15, two leading mantissa bits), so the copy
-// is exact.  One thread per 16 input bytes: x indexes the 16-byte chunks of a
-// head (a row holds 2^lcpr of them, so no division per chunk), y strides over
-// the heads.
 // Zeroes `words` 32-bit words (the no-allocation entry point's queue
 // counters) in stream order; a kernel rather than a memset so that graph
 // capture records a kernel node.
 __global__ void __launch_bounds__(64) clear_words(uint32_t* __restrict__ p, int words) {
     for (int i = threadIdx.x; i < words; i += blockDim.x) p[i] = 0u;
-}
-
-__global__ void __launch_bounds__(256) widen_v8(const uint8_t* __restrict__ v, int64_t sz, int64_t sh,
-                                                int64_t sn, int32_t h, int32_t nh, int32_t lcpr,
-                                                int64_t per_head, uint32_t* __restrict__ out) {
-    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;  // chunk inside the head
-    if (c >= per_head) return;
-    const int64_t m = c >> lcpr;
-    const int ch = (int)(c & ((1 << lcpr) - 1));
-    for (int bh = blockIdx.y; bh < nh; bh += gridDim.y) {
-        const int z = bh / h;
-        const int hh = bh - z * h;
-        const uint4 w = *(const uint4*)(v + z * sz + hh * sh + m * sn + ch * 16);
-        const uint32_t in[4] = {w.x, w.y, w.z, w.w};
-        uint32_t o[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[2 * i] = ((in[i] << 8) & 0xFF00u) | ((in[i] << 16) & 0xFF000000u);
-            o[2 * i + 1] = ((in[i] >> 8) & 0xFF00u) | (in[i] & 0xFF000000u);
-        }
-        uint4* dst = (uint4*)(out + ((int64_t)bh * per_head + c) * 8);
-        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
-    }
 }
 
 }  // namespace
@@ -407,11 +377,10 @@ const char* rsfa_strerror(int status) {
         case RSFA_E_LAUNCH: return "kernel launch failed";
         case RSFA_E_ABI: return "rsfa_fwd_args.struct_size does not match this library";
         case RSFA_E_SCRATCH:
-            return "the problem needs more workspace (float8 V copy plus split state) than the no-allocation "
+            return "the problem needs more workspace (split state) than the no-allocation "
                    "entry point's fixed buffer (RSFA_NOALLOC_WORKSPACE_BYTES)";
         case RSFA_E_WORKSPACE:
-            return "workspace missing or smaller than rsfa_v8_workspace_bytes() (float8 V) plus "
-                   "rsfa_split_workspace_bytes() (causal split mode)";
+            return "workspace missing or smaller than rsfa_split_workspace_bytes() (causal split mode)";
         default: return "unknown rsfa status";
     }
 }
@@ -455,14 +424,8 @@ int rsfa_get_tiling(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32
     return RSFA_OK;
 }
 
-// Whether a float8 V is read as bytes by the kernels (head dims 64, 128 and
-// 256) rather than from an fp16 copy.
-static bool v8_native(int64_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
-
-uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim) {
-    if (z < 1 || h < 1 || n_ctx < 1 || !valid_head_dim(head_dim) || v8_native(head_dim)) return 0;
-    return (uint64_t)(z * h * n_ctx * head_dim) * 2;
-}
+// The kernels read a float8 V's bytes at every head dim: no copy, no workspace.
+uint64_t rsfa_v8_workspace_bytes(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx, int64_t head_dim, int32_t block_m) {
     if (z < 1 || h < 1 || n_ctx < 1 || block_m < 1 || !valid_head_dim(head_dim)) return 0;
@@ -516,7 +479,7 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
     // a float8 V is read from its fp16 copy, except at head dims 64, 128 and
     // 256 (bytes, whose offsets are half those of the fp16 check)
-    const int64_t v_rows = v8 && !v8_native(a->head_dim) ? a->head_dim : a->v_stride[2];
+    const int64_t v_rows = a->v_stride[2];
     for_each_kernel([&](const KernelEntry& e) {
         const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS
         if (st == RSFA_OK && e.dtype == a->dtype && e.d == a->head_dim &&
@@ -564,34 +527,14 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     if (p.c < FLT_MIN) p.c = FLT_MIN;
     p.neg = sc < 0.0f ? 1u : 0u;
 
-    // workspace: the fp16 copy of a float8 V first, then the split state
-    const bool v8_copy = v8 && !v8_native(a->head_dim);
-    const uint64_t v8_bytes = v8_copy ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
-    if (v8_copy || split) {
-        const uint64_t need =
-            v8_bytes + (split ? rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm) : 0);
+    // workspace: the split state
+    if (split) {
+        const uint64_t need = rsfa_split_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim, bm);
         if (!ws || ws_bytes < need) return RSFA_E_WORKSPACE;
-        if (((uintptr_t)ws & (v8_copy ? 15 : 3)) != 0) return RSFA_E_ALIGN;
-        if (split) {
-            // (m, l) of every row, then the rows' fp32 accumulators
-            p.state = (float*)((char*)ws + v8_bytes);
-            p.acc = p.state + 2 * (int64_t)p.num_tasks * bm;
-        }
-    }
-    if (v8_copy) {
-        uint32_t* wide = (uint32_t*)ws;
-        const int lcpr = a->head_dim == 16 ? 0 : a->head_dim == 32 ? 1 : a->head_dim == 64 ? 2
-                         : a->head_dim == 128 ? 3 : 4;  // log2 of the 16-byte chunks per row
-        const int64_t per_head = a->n_ctx << lcpr;
-        const int32_t nh = (int32_t)(a->z * a->h);
-        const dim3 grid((unsigned)((per_head + 255) / 256), (unsigned)std::min<int64_t>(nh, 65535));
-        hipLaunchKernelGGL(widen_v8, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a->v,
-                           a->v_stride[0], a->v_stride[1], a->v_stride[2], (int32_t)a->h, nh, lcpr, per_head, wide);
-        if (hipGetLastError() != hipSuccess) return RSFA_E_LAUNCH;
-        p.v = wide;
-        p.v_sn = a->head_dim;
-        p.v_sh = a->n_ctx * a->head_dim;
-        p.v_sz = a->h * p.v_sh;
+        if (((uintptr_t)ws & 3) != 0) return RSFA_E_ALIGN;
+        // (m, l) of every row, then the rows' fp32 accumulators
+        p.state = (float*)ws;
+        p.acc = p.state + 2 * (int64_t)p.num_tasks * bm;
     }
 
     const bool dynamic = !(a->flags & RSFA_FLAG_STATIC_SCHEDULE) && (tickets_given || dynamic_schedule_allowed(stream));
@@ -631,9 +574,8 @@ int rsfa_attention_fwd_noalloc(const rsfa_fwd_args* a, void* stream) {
     // Workspace this call needs, checked before any device work (fwd_launch
     // repeats every other check).
     if (valid_dtype(a->dtype) && valid_head_dim(a->head_dim) && a->z >= 1 && a->h >= 1 && a->n_ctx >= 1) {
-        const bool v8 = a->dtype == RSFA_DTYPE_F16_V8E5M2;
         const bool split = a->causal != 0 && (a->flags & RSFA_FLAG_CAUSAL_SPLIT);
-        uint64_t need = v8 ? rsfa_v8_workspace_bytes(a->z, a->h, a->n_ctx, a->head_dim) : 0;
+        uint64_t need = 0;
         if (split) {
             const KernelEntry* e = nullptr;
             if (launch_tile(a, planning_cus(), &e) == RSFA_OK)

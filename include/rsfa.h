@@ -16,11 +16,10 @@
  *   rsfa_resolve_tiling       -> the (BLOCK_M, BLOCK_N) meta-parameters the
  *                                reference passes to _attn_fwd[grid] (518-519, 606-607)
  *   rsfa_get_num_compute_cores-> get_num_compute_cores(), 19-21
- *   rsfa_v8_workspace_bytes   -> (no separate counterpart: the size of the
- *                                fp16 copy of a float8 V, for the fp8_v
- *                                branch of _attn_fwd_inner, 208-211; zero
- *                                at head dims 64, 128 and 256, which read
- *                                V's bytes)
+ *   rsfa_v8_workspace_bytes   -> (no counterpart: workspace a float8 V needs,
+ *                                for the fp8_v branch of _attn_fwd_inner,
+ *                                208-211; zero, the kernels read V's bytes;
+ *                                kept so that callers of ABI version 5 link)
  *   rsfa_strerror             -> (no counterpart: the reference raises Python
  *                                exceptions; codes map to them in the wrapper)
  *
@@ -48,7 +47,7 @@
 extern "C" {
 #endif
 
-#define RSFA_ABI_VERSION 5
+#define RSFA_ABI_VERSION 6
 
 typedef enum rsfa_status {
     RSFA_OK          = 0,
@@ -61,8 +60,7 @@ typedef enum rsfa_status {
     RSFA_E_DEVICE    = -7,  /* HIP runtime error while querying or preparing    */
     RSFA_E_LAUNCH    = -8,  /* kernel launch failed                             */
     RSFA_E_ABI       = -9,  /* struct_size does not match this library          */
-    RSFA_E_WORKSPACE = -10, /* split mode or a float8 V without a large enough
-                               workspace                                        */
+    RSFA_E_WORKSPACE = -10, /* split mode without a large enough workspace       */
     RSFA_E_SCRATCH   = -11  /* rsfa_attention_fwd_noalloc: the problem needs
                                more workspace than RSFA_NOALLOC_WORKSPACE_BYTES */
 } rsfa_status;
@@ -74,12 +72,10 @@ typedef enum rsfa_dtype {
                                     5 exponent bits, bias 15, 2 mantissa bits).
                                     P is rounded to e5m2 for P.V and the row
                                     sums add the unrounded P, as the reference's
-                                    fp8_v branch does (208-211, 217).  At head
-                                    dims 64, 128 and 256 the kernels read V's
-                                    bytes and run P.V on the e5m2 MFMA (no
-                                    workspace); at head dims 16 and 32 the
-                                    library first widens V to fp16 (exactly)
-                                    in `workspace`: see rsfa_v8_workspace_bytes */
+                                    fp8_v branch does (208-211, 217).  The
+                                    kernels read V's bytes and run P.V on the
+                                    e5m2 MFMA at every head dim (no
+                                    workspace) */
 } rsfa_dtype;
 
 /* flags (bit set) */
@@ -113,9 +109,8 @@ typedef struct rsfa_fwd_args {
     float      *lse;          /* optional [Z, H, N_CTX] fp32, natural-log
                                  logsumexp of the scaled scores (the reference's
                                  M = m + ln(l), 400-403); NULL = not written    */
-    void       *workspace;    /* split mode and/or a float8 V: the fp16 copy of
-                                 V (rsfa_v8_workspace_bytes) first, then the
-                                 split state (rsfa_split_workspace_bytes)      */
+    void       *workspace;    /* split mode: the split state
+                                 (rsfa_split_workspace_bytes)                  */
     uint64_t    workspace_bytes;
     int64_t     z, h, n_ctx, head_dim;
     int64_t     q_stride[4];  /* element strides of dims (Z, H, N_CTX, D)       */
@@ -141,8 +136,8 @@ typedef struct rsfa_fwd_args {
  * Replaces _attention.forward (flash_attention_forward.py:547-616). */
 int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
 
-/* Workspace rsfa_attention_fwd_noalloc has for a float8 V copy and the split
- * state (its fixed per-device buffer holds 4 KiB of queue counters besides). */
+/* Workspace rsfa_attention_fwd_noalloc has for the split state (its fixed
+ * per-device buffer holds 4 KiB of queue counters besides). */
 #define RSFA_NOALLOC_WORKSPACE_BYTES (16u << 20)
 
 /* rsfa_attention_fwd without any allocation.  It has no counterpart in the
@@ -150,7 +145,7 @@ int rsfa_attention_fwd(const rsfa_fwd_args *args, void *stream);
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same arguments, kernels and results as rsfa_attention_fwd, except that
  * `workspace`/`workspace_bytes` are ignored: the queue counters and the
- * workspace (a float8 V's fp16 copy, the split state) live in one fixed
+ * workspace (the split state) live in one fixed
  * buffer per device, a static device array of RSFA_NOALLOC_WORKSPACE_BYTES
  * + 4 KiB that the device holds until the process ends.  Problems that need
  * more workspace fail with RSFA_E_SCRATCH before any device work.  The first
@@ -171,11 +166,10 @@ int rsfa_attention_fwd_noalloc(const rsfa_fwd_args *args, void *stream);
 uint64_t rsfa_split_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                     int64_t head_dim, int32_t block_m);
 
-/* Bytes of workspace a float8 V (RSFA_DTYPE_F16_V8E5M2) needs: the fp16 copy
- * of V, contiguous [Z, H, N_CTX, D], at head dims 16 and 32, or 0 at head
- * dims 64, 128 and 256 (their kernels read the float8 bytes).  Split mode adds its state after it, at
- * this offset.
- * 0 for invalid sizes. */
+/* Bytes of workspace a float8 V (RSFA_DTYPE_F16_V8E5M2) needs: 0 (the kernels
+ * read the float8 bytes at every head dim).  ABI version 5 placed an fp16
+ * copy of V at head dims 16 and 32 here, before the split state; version 6
+ * has none, and the split state starts at the workspace's first byte. */
 uint64_t rsfa_v8_workspace_bytes(int64_t z, int64_t h, int64_t n_ctx,
                                  int64_t head_dim);
 

@@ -90,11 +90,10 @@ def test_strided_float8_v_matches_contiguous():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("D", [64, 128, 32])
+@pytest.mark.parametrize("D", [64, 128, 32, 16])
 def test_split_mode_with_float8_v(D):
-    """The two-launch causal split with a float8 V: the byte path (D = 64,
-    128) and the fp16 copy (D = 32), the copy then the split state in one
-    workspace."""
+    """The two-launch causal split with a float8 V on the byte path (the split
+    state alone in the workspace)."""
     q, k, v = A.make_inputs(1, 4, 700, D, seed=17)
     v8 = v.to(torch.float8_e5m2)
     o = _run(q, k, v8, True, 0.25, split=True)
@@ -140,29 +139,27 @@ def test_workspace_size_and_alignment_are_checked_before_any_launch():
     from ascend_rsfa import _native
 
     lib = _native.lib()
-    # head dim 32: a float8 V goes through its fp16 copy (64 and 128 read the bytes)
+    # a float8 V needs no workspace at any head dim; the causal split needs its state
     q, k, v = (t.cuda() for t in A.make_inputs(1, 2, 128, 32, seed=23))
     v8, o = v.to(torch.float8_e5m2), torch.empty_like(q)
-    need = int(lib.rsfa_v8_workspace_bytes(1, 2, 128, 32))
-    assert need > 0 and lib.rsfa_v8_workspace_bytes(1, 2, 128, 64) == 0
-    ws = torch.empty(need // 4 + 16, dtype=torch.float32, device="cuda")
+    assert all(lib.rsfa_v8_workspace_bytes(1, 2, 128, d) == 0 for d in (16, 32, 64, 128, 256))
     run = lambda a: lib.rsfa_attention_fwd(ctypes.byref(a), None)  # noqa: E731
     print("workspace checks", flush=True)
-    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2)) == _native.E_WORKSPACE
-    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, ws=ws.data_ptr(), ws_bytes=need - 16)) == \
-        _native.E_WORKSPACE
-    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, ws=ws.data_ptr() + 4, ws_bytes=need)) == \
-        _native.E_ALIGN
-    # causal split: the state after the float8 V copy, both counted
+    assert run(_raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2)) == _native.OK
     split = int(lib.rsfa_split_workspace_bytes(1, 2, 128, 32, 128))
-    assert run(_raw_args(q, k, q, o, 0, causal=True, flags=_native.FLAG_CAUSAL_SPLIT)) == _native.E_WORKSPACE
-    big = torch.empty((need + split) // 4 + 16, dtype=torch.float32, device="cuda")
-    a = _raw_args(q, k, v8, o, _native.DTYPE_F16_V8E5M2, causal=True, flags=_native.FLAG_CAUSAL_SPLIT,
-                  ws=big.data_ptr(), ws_bytes=need + split - 4)
-    a.block_m, a.block_n = 128, 64
-    assert run(a) == _native.E_WORKSPACE
+    ws = torch.empty(split // 4 + 16, dtype=torch.float32, device="cuda")
+    for vv, code in ((q, _native.DTYPE_F16), (v8, _native.DTYPE_F16_V8E5M2)):
+        a = _raw_args(q, k, vv, o, code, causal=True, flags=_native.FLAG_CAUSAL_SPLIT)
+        a.block_m, a.block_n = 128, 64
+        assert run(a) == _native.E_WORKSPACE
+        a.workspace, a.workspace_bytes = ws.data_ptr(), split - 4
+        assert run(a) == _native.E_WORKSPACE
+        a.workspace, a.workspace_bytes = ws.data_ptr() + 2, split
+        assert run(a) == _native.E_ALIGN
+        a.workspace, a.workspace_bytes = ws.data_ptr(), split
+        assert run(a) == _native.OK
     msg = lib.rsfa_strerror(_native.E_WORKSPACE).decode()
-    assert "rsfa_v8_workspace_bytes" in msg and "rsfa_split_workspace_bytes" in msg
+    assert "rsfa_split_workspace_bytes" in msg
     torch.cuda.synchronize()
 
 
@@ -188,8 +185,8 @@ def test_uncompiled_tile_request_within_the_rounding_bound(N):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("N,scale", [(1024, 0.1), (777, -0.3)])
 def test_byte_v_tiles_within_the_rounding_bound(D, tile, causal, N, scale):
-    """Head dims 64 and 128 read a float8 V's bytes into LDS (no fp16 copy)
-    and run P.V on the e5m2 MFMA: every compiled tile (D=128: ping-pong
+    """A float8 V's bytes go into LDS and P.V runs on the e5m2 MFMA: at head
+    dims 64 and 128 every compiled tile (D=128: ping-pong
     (256, 64), (256, 128), the 4-wave (128, 64); D=64: ping-pong (256, 128),
     4-wave (128, 64)), whole and ragged key tiles, a negative scale, more tasks
     than workgroups, against the exact result within the per-element bound of
@@ -262,15 +259,24 @@ def _byte_tiles(D, causal):
 
 
 def _peaked_inputs(N, D, causal, seed):
-    """Query i attends to key pi(i) alone: K rows are random +-1, Q[i] =
-    K[pi(i)], and sm_scale 1, so the score of pi(i) is D while every other
-    visible key scores at most D - 30 / log2(e) (checked here in float64):
-    every other P is below 2^-30 of P[pi(i)] = 1.  V rows are distinct e5m2
-    values, so O[i] = V[pi(i)] exactly names the key the kernel paired with
-    row i.  Non-causal pi is a permutation (every key position of every
-    64-key MFMA group and tile once); causal pi(i) in [i - 63, i]."""
+    """Query i attends to key pi(i) alone: K rows are distinct random +-1
+    rows, Q[i] = K[pi(i)], so the score of pi(i) is D while every other key
+    scores at most D - 2; sm_scale (1 from D = 64 on, 16 below, returned) puts
+    every other visible key at least 30 log2 units below (checked here in
+    float64): every other P is below 2^-30 of P[pi(i)] = 1.  V rows are
+    distinct e5m2 values, so O[i] = V[pi(i)] exactly names the key the kernel
+    paired with row i.  Non-causal pi is a permutation (every key position of
+    every 64-key MFMA group and tile once); causal pi(i) in [i - 63, i]."""
     g = torch.Generator().manual_seed(seed)
+    scale = 1.0 if D >= 64 else 16.0
     k = (torch.randint(0, 2, (N, D), generator=g) * 2 - 1).float()
+    for _ in range(64):  # re-draw repeated rows (likely at D = 16)
+        _, inv, cnt = torch.unique(k, dim=0, return_inverse=True, return_counts=True)
+        rep_rows = torch.nonzero(torch.tensor([bool(cnt[inv[i]] > 1) and bool((inv[:i] == inv[i]).any())
+                                               for i in range(N)])).flatten()
+        if rep_rows.numel() == 0:
+            break
+        k[rep_rows] = (torch.randint(0, 2, (rep_rows.numel(), D), generator=g) * 2 - 1).float()
     if causal:
         pi = torch.tensor([i - int(torch.randint(0, min(i, 63) + 1, (1,), generator=g)) for i in range(N)])
     else:
@@ -281,26 +287,26 @@ def _peaked_inputs(N, D, causal, seed):
         s.masked_fill_(A.causal_mask(N), float("-inf"))
     top = s.gather(1, pi[:, None]).squeeze(1)
     others = s.scatter(1, pi[:, None], float("-inf")).max(dim=1).values
-    assert bool((top == D).all()) and bool(((top - others) * 1.4426950408889634 >= 30).all()), \
+    assert bool((top == D).all()) and bool(((top - others) * scale * 1.4426950408889634 >= 30).all()), \
         "construction: a row's peak is not 30 log2 units above its other keys"
     v8 = torch.from_numpy(A.round_e5m2((torch.randn(N, D, generator=g) * 2).numpy())).to(torch.float8_e5m2)
     assert len({tuple(r) for r in v8.view(torch.uint8).tolist()}) == N, "V rows must be distinct"
-    return q.half()[None, None], k.half()[None, None], v8[None, None], pi
+    return q.half()[None, None], k.half()[None, None], v8[None, None], pi, scale
 
 
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("N", [64, 273, 1024])
 def test_peaked_rows_return_their_key_value_on_every_tile(D, causal, N):
-    """Known answers for the float8 V P.V path on every compiled tile: head
-    dims 64 and 128 read V's bytes (byte-transposing reads, swizzled 16-byte
-    chunks, P and V paired byte by byte inside each 64-key MFMA), head dim
-    256 its fp16 copy.  A key read from the wrong row, chunk, lane or 16-key
-    group gives another row's V."""
-    q, k, v8, pi = _peaked_inputs(N, D, causal, seed=1000 + N + D + causal)
+    """Known answers for the float8 V P.V path on every compiled tile of
+    every head dim: V's bytes in LDS (byte-transposing reads, 16-byte chunks
+    swizzled from 64-byte rows on, 32-byte rows with the D = 16 filler chunk),
+    P and V paired byte by byte inside each 64-key MFMA.  A key read from the
+    wrong row, chunk, lane or 16-key group gives another row's V."""
+    q, k, v8, pi, scale = _peaked_inputs(N, D, causal, seed=1000 + N + D + causal)
     want = v8[0, 0].float()[pi]
     for tile in _byte_tiles(D, causal):
-        o = _run(q, k, v8, causal, 1.0, BM=tile[0], BN=tile[1])[0, 0]
+        o = _run(q, k, v8, causal, scale, BM=tile[0], BN=tile[1])[0, 0]
         bad = (o - want).abs() > 2.0 ** -10 * want.abs()
         assert not bool(bad.any()), (f"tile {tile}: {int(bad.any(dim=1).sum())} of {N} rows differ from "
                                      f"V[pi(i)], first row {int(bad.any(dim=1).nonzero()[0])}")
@@ -344,9 +350,8 @@ def test_exact_row_max_matches_the_rounded_p_oracle(D, causal, N):
     """With the row max on key 0 and scores on a 1/8 grid the kernel rounds
     exactly the P the oracle rounds (reference_attention_fp8v: P = 2^(-j/8),
     1 -> 1, 0.917 -> 0.875, ...), so O must match it to fp16 rounding, not
-    just within the loose per-element rounding bound: on the byte tiles
-    (D = 64, 128) and the fp16-copy path (D = 16, 32, 256), at lengths whose
-    last 64-key group is partial."""
+    just within the loose per-element rounding bound: on every byte tile of
+    every head dim, at lengths whose last 64-key group is partial."""
     Z, H = 1, 2
     q, k, v8 = _first_key_max_inputs(Z, H, N, D, seed=2000 + N + D)
     scale = float(np.log(2.0))

@@ -35,8 +35,7 @@ def _args(q, k, v, o, lse, causal, scale, dtype_code, flags=0, ws=None):
 
 def _workspace_bytes(lib, a):
     """What rsfa_attention_fwd needs for `a`, with the tile its launch picks."""
-    v8 = a.dtype == _native.DTYPE_F16_V8E5M2
-    n = int(lib.rsfa_v8_workspace_bytes(a.z, a.h, a.n_ctx, a.head_dim)) if v8 else 0
+    n = 0  # a float8 V needs none
     if a.causal and a.flags & _native.FLAG_CAUSAL_SPLIT:
         bm, bn = ctypes.c_int32(), ctypes.c_int32()
         assert lib.rsfa_get_tiling(a.z, a.h, a.n_ctx, a.head_dim, a.causal, a.dtype,
@@ -164,15 +163,15 @@ def _cpu_args(n=8192, d=128, **over):
 def test_noalloc_rejects_problems_beyond_its_buffer_before_device_work():
     lib = _native.lib()
     limit = _native.NOALLOC_WORKSPACE_BYTES
-    # a float8 V's fp16 copy is 2*Z*H*N*D bytes: 1x8x32768x32 is exactly the limit
-    fits = _cpu_args(n=32768, d=32, dtype=_native.DTYPE_F16_V8E5M2)
-    assert lib.rsfa_v8_workspace_bytes(1, 8, 32768, 32) == limit
-    over = _cpu_args(n=32768, d=32, dtype=_native.DTYPE_F16_V8E5M2, z=2)
+    # split state: (2 + 64) fp32 per query row; 63488 rows (a multiple of
+    # every BLOCK_M) fit the limit, 63744 do not
+    fits = _cpu_args(z=1, h=1, n=63488, d=64, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
+    assert lib.rsfa_split_workspace_bytes(1, 1, 63488, 64, 256) == 63488 * 66 * 4 <= limit
+    over = _cpu_args(z=1, h=1, n=63744, d=64, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
+    assert lib.rsfa_split_workspace_bytes(1, 1, 63744, 64, 256) > limit
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(over), None) == _native.E_SCRATCH
-    # at head dims 64, 128 and 256 the kernels read a float8 V's bytes: no copy, any size
-    assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 128) == 0
-    assert lib.rsfa_v8_workspace_bytes(2, 8, 8192, 256) == 0
-    big_v8 = _cpu_args(dtype=_native.DTYPE_F16_V8E5M2, z=2)
+    # a float8 V needs no workspace at any size or head dim
+    big_v8 = _cpu_args(n=32768, d=32, dtype=_native.DTYPE_F16_V8E5M2, z=2)
     # split state: (2 + head_dim) fp32 per query row, rounded to the tile
     split = _cpu_args(z=8, h=32, n_ctx=16384, causal=1, flags=_native.FLAG_CAUSAL_SPLIT)
     assert lib.rsfa_attention_fwd_noalloc(ctypes.byref(split), None) == _native.E_SCRATCH
