@@ -1,0 +1,82 @@
+"""Seeded sweep over the launch space: random shapes (ragged and whole query
+and key tiles, one to thousands of keys), every head dim, fp16 / bf16 /
+float8-V, causal or not, scales of either sign, a tile request or none, the
+scheduling and split flags, and strided [B, S, H, D] views, each case against
+the oracle's closed form.  The case list is drawn once from a fixed seed, so a
+failure names a reproducible case."""
+import math
+import random
+
+import pytest
+import torch
+
+from ascend_rsfa import flash_attention_forward as F
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 1e-2
+_POW2 = [16, 32, 64, 128, 256, 512]
+
+
+def _draw_cases(n, seed=20261202):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        D = rng.choice([16, 32, 64, 128, 256])
+        kind = rng.choice(["f16", "f16", "bf16", "v8"])
+        causal = rng.random() < 0.5
+        N = rng.choice([1, 2, 17, 63, 64, 65, 127, 128, 255, 256, 257, 300, 511, 640, 1000, 1023, 1536, 2049])
+        Z, H = rng.randint(1, 3), rng.randint(1, 9)
+        scale = rng.choice([1 / math.sqrt(D), 0.5, -0.7, 2.0, rng.uniform(-1.5, 1.5)])
+        if rng.random() < 0.5:
+            tile = (0, 0)
+        else:
+            while True:
+                bm, bn = rng.choice(_POW2), rng.choice(_POW2)
+                if bm * bn <= 65536 and not (causal and bn > bm):
+                    break
+            tile = (bm, bn)
+        split = causal and rng.random() < 0.3
+        static = rng.random() < 0.25
+        single = causal and rng.random() < 0.3
+        bshd = rng.random() < 0.3
+        cases.append(dict(i=i, Z=Z, H=H, N=N, D=D, kind=kind, causal=causal, scale=scale, tile=tile,
+                          split=split, static=static, single=single, bshd=bshd))
+    return cases
+
+
+CASES = _draw_cases(200)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"case{c['i']:02d}" for c in CASES])
+def test_random_launch(case):
+    c = case
+    print(f"sweep {c}", flush=True)
+    Z, H, N, D = c["Z"], c["H"], c["N"], c["D"]
+    dtype = torch.bfloat16 if c["kind"] == "bf16" else torch.float16
+    q, k, v = A.make_inputs(Z, H, N, D, seed=1000 + c["i"], dtype=dtype)
+    if c["kind"] == "v8":
+        v = v.to(torch.float8_e5m2)
+    dev = []
+    for t in (q, k, v):
+        if c["bshd"]:
+            # [B, S, H, D] storage viewed as [B, H, S, D]
+            t = t.permute(0, 2, 1, 3).contiguous().cuda().permute(0, 2, 1, 3)
+        else:
+            t = t.cuda()
+        dev.append(t)
+    o = F.forward(*dev, c["causal"], c["scale"], *c["tile"], exact_tile=c["tile"] != (0, 0),
+                  split=c["split"], static_schedule=c["static"], single_blocks=c["single"])
+    torch.cuda.synchronize()
+    out = o.float().cpu()
+    assert torch.isfinite(out).all()
+    if c["kind"] == "v8":
+        exact = A.reference_attention(q, k, v.float(), c["causal"], c["scale"])
+        bound = A.fp8v_error_bound(q, k, v, c["causal"], c["scale"])
+        excess = ((out - exact).abs() - bound).max().item()
+        assert excess <= 0, f"case {c['i']}: outside the e5m2 rounding bound by {excess:.3e}"
+    else:
+        ref = A.reference_attention(q, k, v, c["causal"], c["scale"])
+        err = (out - ref).abs().max().item()
+        assert torch.allclose(out, ref, atol=ATOL, rtol=RTOL), f"case {c['i']}: max |err| = {err:.3e}"
