@@ -118,7 +118,7 @@ def get_tiling(Z, H, N_CTX, HEAD_DIM, causal, dtype=torch.float16):
     on the current device's CUs, so it answers for every valid shape.
     ``attention`` called with this tile (or with ``BM = BN = 0``) runs it.
     """
-    cache = _package_module("tiling").active_cache()
+    cache = _tiling_module().active_cache()
     if cache is not None:
         entry = cache.lookup(Z, H, N_CTX, HEAD_DIM, causal, dtype)
         if entry is not None:
@@ -190,6 +190,50 @@ def _hint_mode(tile_hint, exact_tile):
     return os.environ.get("RSFA_TILE_HINT", "").strip().lower() in ("1", "true", "yes", "on")
 
 
+_PLANS = {}
+_TILING = None
+
+
+def _tiling_module():
+    global _TILING
+    if _TILING is None:
+        _TILING = _package_module("tiling")
+    return _TILING
+
+
+def _make_plan(q_, k_, v_, o, v8, causal, BM, BN, hint, split, static_schedule, single_blocks):
+    """The launch arguments of a call but its pointers and scale (a byte copy
+    of rsfa_fwd_args), and the workspace bytes it needs; on the current
+    device, which must be the tensors' device."""
+    Z, H, N, D = q_.shape
+    lib = _native.lib()
+    # The tile is settled here and passed as an exact request, so the
+    # launch runs the same tile the split workspace is sized for, and a
+    # get_tiling answer from a measured cache is honoured.
+    if (BM or BN) and not hint:
+        bm, bn = resolve_tiling(D, causal, BM, BN, q_.dtype)
+    else:
+        if BM or BN:
+            resolve_tiling(D, causal, BM, BN, q_.dtype)  # the reference's validity rules
+        bm, bn = get_tiling(Z, H, N, D, causal, q_.dtype)
+    args = _native.FwdArgs()
+    args.struct_size = ctypes.sizeof(_native.FwdArgs)
+    args.dtype = _native.DTYPE_F16_V8E5M2 if v8 else _DTYPES[q_.dtype]
+    args.z, args.h, args.n_ctx, args.head_dim = Z, H, N, D
+    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
+        getattr(args, name)[:] = list(t.stride())
+    args.causal = 1 if causal else 0
+    args.block_m = bm
+    args.block_n = bn
+    args.flags = _native.FLAG_EXACT_TILE | (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
+        _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0) | (
+        _native.FLAG_SINGLE_BLOCKS if single_blocks else 0)
+    nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0  # 0: the kernels read the bytes
+    if split and causal:
+        nbytes += split_workspace_bytes(Z, H, N, D, bm)
+    return bytes(args), nbytes
+
+
 def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=False,
             static_schedule=False, single_blocks=False, tile_hint=None, exact_tile=False, out=None):
     """Run the forward kernel; returns ``o`` or ``(o, lse)``.
@@ -221,7 +265,6 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
     if not (q.is_cuda and k.is_cuda and v.is_cuda) or not (q.device == k.device == v.device):
         raise ValueError("q, k and v must be GPU tensors on one device")
     Z, H, N, D = q.shape
-    lib = _native.lib()
     q_, k_, v_ = _as_kernel_layout(q), _as_kernel_layout(k), _as_kernel_layout(v)
     if out is None:
         o = torch.empty_like(q_)
@@ -231,42 +274,44 @@ def forward(q, k, v, causal, sm_scale, BM=0, BN=0, *, return_lse=False, split=Fa
             raise ValueError("out must match q's shape, dtype and device and have a unit-stride head dim")
     lse = torch.empty((Z, H, N), dtype=torch.float32, device=q.device) if return_lse else None
 
-    args = _native.FwdArgs()
-    args.struct_size = ctypes.sizeof(_native.FwdArgs)
-    args.dtype = _native.DTYPE_F16_V8E5M2 if v8 else _DTYPES[q.dtype]
+    dev = q.device.index
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    hint = _hint_mode(tile_hint, exact_tile) if (BM or BN) else False
+    # The launch arguments but the pointers and the scale depend only on the
+    # call's shapes, strides, types and options: memoised while no measured
+    # tiling cache is active (its answers may change between calls).
+    key = None
+    if _tiling_module().active_cache() is None:
+        key = (Z, H, N, D, q_.dtype, v8, bool(causal), int(BM), int(BN), hint, bool(split),
+               bool(static_schedule), bool(single_blocks), dev, q_.stride(), k_.stride(), v_.stride(), o.stride())
+    plan = _PLANS.get(key) if key is not None else None
+    if plan is None:
+        if dev == torch.cuda.current_device():
+            plan = _make_plan(q_, k_, v_, o, v8, causal, BM, BN, hint, split, static_schedule, single_blocks)
+        else:
+            with torch.cuda.device(q.device):
+                plan = _make_plan(q_, k_, v_, o, v8, causal, BM, BN, hint, split, static_schedule, single_blocks)
+        if key is not None:
+            if len(_PLANS) > 4096:
+                _PLANS.clear()
+            _PLANS[key] = plan
+    template, nbytes = plan
+    args = _native.FwdArgs.from_buffer_copy(template)
     args.q, args.k, args.v, args.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
     args.lse = lse.data_ptr() if lse is not None else None
-    args.z, args.h, args.n_ctx, args.head_dim = Z, H, N, D
-    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
-        getattr(args, name)[:] = list(t.stride())
     args.sm_scale = float(sm_scale)
-    args.causal = 1 if causal else 0
     ws = None
-    with torch.cuda.device(q.device):
-        # The tile is settled here and passed as an exact request, so the
-        # launch runs the same tile the split workspace is sized for, and a
-        # get_tiling answer from a measured cache is honoured.
-        if (BM or BN) and not _hint_mode(tile_hint, exact_tile):
-            bm, bn = resolve_tiling(D, causal, BM, BN, q.dtype)
-        else:
-            if BM or BN:
-                resolve_tiling(D, causal, BM, BN, q.dtype)  # the reference's validity rules
-            bm, bn = get_tiling(Z, H, N, D, causal, q.dtype)
-        args.block_m = bm
-        args.block_n = bn
-        args.flags = _native.FLAG_EXACT_TILE | (_native.FLAG_STATIC_SCHEDULE if static_schedule else 0) | (
-            _native.FLAG_CAUSAL_SPLIT if (split and causal) else 0) | (
-            _native.FLAG_SINGLE_BLOCKS if single_blocks else 0)
-        # workspace: a float8 V needs none (rsfa_v8_workspace_bytes is 0); the split state
-        nbytes = int(lib.rsfa_v8_workspace_bytes(Z, H, N, D)) if v8 else 0
-        if split and causal:
-            nbytes += split_workspace_bytes(Z, H, N, D, bm)
-        if nbytes:
-            ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
-            args.workspace = ws.data_ptr()
-            args.workspace_bytes = nbytes
-        stream = torch.cuda.current_stream(q.device).cuda_stream
+    if nbytes:
+        # workspace: the split state (a float8 V needs none)
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = nbytes
+    lib = _native.lib()
+    if dev == torch.cuda.current_device():
         st = lib.rsfa_attention_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    else:
+        with torch.cuda.device(q.device):
+            st = lib.rsfa_attention_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
     _raise_for(st)
     if out is not None and o is not out:
         out.copy_(o)
