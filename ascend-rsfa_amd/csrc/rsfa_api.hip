@@ -477,13 +477,11 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
     // launch could pick (before any device work): the K/V loader's per-lane
     // 32-bit offsets, and the split state's 32-bit rows (task * BLOCK_M + row
     // <= Z*H*N_CTX rounded up to the largest BLOCK_M, 256).
-    // a float8 V is read from its fp16 copy, except at head dims 64, 128 and
-    // 256 (bytes, whose offsets are half those of the fp16 check)
-    const int64_t v_rows = a->v_stride[2];
+    // (a float8 V's byte offsets are half those of the two-byte check)
     for_each_kernel([&](const KernelEntry& e) {
         const bool q_loader = uses_q_buffer(e.d, e.bn, e.nw, e.causal != 0, e.mode);  // Q through LDS
         if (st == RSFA_OK && e.dtype == a->dtype && e.d == a->head_dim &&
-            (!loader_offsets_fit(e, a->k_stride[2]) || !loader_offsets_fit(e, v_rows) ||
+            (!loader_offsets_fit(e, a->k_stride[2]) || !loader_offsets_fit(e, a->v_stride[2]) ||
              (q_loader && !loader_offsets_fit(e, a->q_stride[2]))))
             st = RSFA_E_ALIGN;
     });
