@@ -27,6 +27,15 @@ window 11 % slow among repeats) does not decide the figure.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--windows N] [--no-cpu]
                     [--only NAME] [--calibrate-copy-mib M] [--device-warmup-s S]
+                    [--no-gpu-reference]
+
+``gpu_reference`` puts the kernel's MFMA fraction in context: in the same run,
+after the timed configs, an fp16 8192^3 GEMM through torch.matmul (the vendor's
+hipBLASLt) and PyTorch's own scaled_dot_product_attention on the headline's
+and the causal target's inputs, each timed like a config (about a second of
+back-to-back calls, then the median of three windows of 10).  It is a
+yardstick of what this GPU sustains under the same power and clock conditions,
+not a baseline the kernel's figures are divided by.
 
 ``--calibrate-copy-mib M`` adds one plain device-to-device copy of M MiB after
 the timed work; under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives
@@ -215,6 +224,64 @@ def roofline(cfg, res):
             "frac": round(achieved / peak, 4), "traffic": traffic, **src}
 
 
+def _median_window_ms(torch, f, warm_s, calls, windows=3):
+    """Median over `windows` windows of `calls` back-to-back calls of f(), in ms
+    per call, after about `warm_s` seconds of back-to-back calls."""
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    while time.perf_counter() - t < warm_s:
+        f()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    win = []
+    for _ in range(windows):
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(calls):
+            f()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        win.append(e0.elapsed_time(e1) / calls)
+    return sorted(win)[(len(win) - 1) // 2]
+
+
+def gpu_reference(torch, sdpa_cases, warm_s=1.0):
+    """What the vendor's own libraries reach on this GPU in the same run, as a
+    yardstick for the MFMA fraction (not a baseline the kernel is measured
+    against): an fp16 GEMM through torch.matmul (hipBLASLt), 8192^3, and
+    PyTorch's scaled_dot_product_attention on the given bench inputs
+    (name, q, k, v, causal, sm_scale), flash backend where available."""
+    import torch.nn.functional as TF
+
+    out = {}
+    n = 8192
+    a = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    ms = _median_window_ms(torch, lambda: a @ b, warm_s, 10)
+    out["gemm_fp16"] = {"shape": [n, n, n], "ms_per_call": round(ms, 4),
+                        "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)}
+    del a, b
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        ctx, backend = (lambda: sdpa_kernel([SDPBackend.FLASH_ATTENTION])), "flash"
+    except ImportError:
+        import contextlib
+        ctx, backend = contextlib.nullcontext, "default"
+    for name, q, k, v, causal, scale in sdpa_cases:
+        B, H, S, D = q.shape
+        try:
+            with ctx():
+                f = lambda: TF.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)  # noqa: E731
+                ms = _median_window_ms(torch, f, warm_s, 10)
+            out["sdpa_" + name] = {"backend": backend, "ms_per_call": round(ms, 4),
+                                   "tflops": round(flops(B, H, S, D, causal) / (ms * 1e-3) / 1e12, 1)}
+        except RuntimeError as e:  # no kernel of that backend for this GPU or shape
+            out["sdpa_" + name] = {"backend": backend, "error": str(e)[:160]}
+    torch.cuda.empty_cache()
+    return out
+
+
 def calibrate_copy(torch, mib):
     """One plain device copy of `mib` MiB (reads and writes mib MiB each)."""
     n = mib * (1 << 20)
@@ -300,6 +367,8 @@ def main():
                     help="windows of --steps timed calls per config; the median window is reported")
     ap.add_argument("--device-warmup-s", type=float, default=DEVICE_WARMUP_S,
                     help="seconds of back-to-back launches before each config (0 under counter passes)")
+    ap.add_argument("--no-gpu-reference", action="store_true",
+                    help="skip the vendor GEMM / PyTorch SDPA yardstick measured after the configs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the path shards by (batch, head) with no "
@@ -333,6 +402,15 @@ def main():
         results[cfg[0]] = time_config(F, torch, cfg, dev, fp_ok, args.steps, args.warmup,
                                       device_warmup_s=args.device_warmup_s, windows=args.windows)
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
+    gref = None
+    if not args.no_gpu_reference:
+        cases = []
+        for cfg in configs:
+            if cfg[0] in (HEADLINE, CAUSAL_TARGET) and len(cfg) <= 8:
+                q, k, v = resident[FINGERPRINT_KEY.get(cfg[0], cfg[0])][0]
+                cases.append((cfg[0], q, k, v, cfg[5], cfg[6]))
+        gref = gpu_reference(torch, cases)
+        print(f"[bench] gpu reference: {gref}", file=sys.stderr, flush=True)
     resident.clear()
     torch.cuda.empty_cache()
     if args.calibrate_copy_mib:
@@ -371,6 +449,10 @@ def main():
         line["causal_target"] = {"workload": f"{CAUSAL_TARGET}: B=128 H=8 S=2048 D=128 causal sm_scale=0.5",
                                  "ms_per_call": rc["ms_per_call"], "tflops": rc["tflops"],
                                  "roofline": roofline(by_name[CAUSAL_TARGET], rc)}
+    if gref is not None:
+        # the headline's rate as a fraction of the vendor fp16 GEMM's on the same GPU
+        gref["value_over_gemm_fp16"] = round(r["tflops"] / gref["gemm_fp16"]["tflops"], 3)
+        line["gpu_reference"] = gref
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, cfg, head_inputs)
     print(json.dumps(line), flush=True)

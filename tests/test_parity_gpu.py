@@ -472,6 +472,31 @@ def test_many_heads_short_rows(causal):
     _assert_close(torch.stack([out[z, h] for z, h in heads]), ref, "many heads")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_tensors_past_4_gib(causal):
+    """Q, K, V and O of 4.4 GB each (Z=132 H=32 N=4096 D=128 fp16): the heads
+    past byte offset 2^32 are addressed through the 64-bit per-task bases
+    (32-bit offsets only inside a key tile), and the row logsumexp of the
+    last head lands at its place.  Heads on both sides of the 4 GiB mark
+    against the CPU oracle."""
+    Z, H, N, D = 132, 32, 4096, 128
+    assert Z * H * N * D * 2 > (1 << 32) + N * D * 2
+    g = torch.Generator(device=DEV).manual_seed(61)
+    q, k, v = (torch.randn((Z, H, N, D), generator=g, device=DEV, dtype=torch.float16) for _ in range(3))
+    print(f"tensors past 4 GiB Z={Z} H={H} N={N} D={D} causal={causal}", flush=True)
+    out, lse = F.forward(q, k, v, causal, 0.1, return_lse=True)
+    torch.cuda.synchronize()
+    # (127, 31) ends at exactly 4 GiB, (128, 0) starts there, (131, 31) is the last head
+    heads = [(0, 0), (127, 31), (128, 0), (131, 31)]
+    ref, ref_lse = A.reference_attention(q, k, v, causal, 0.1, return_lse=True, heads=heads)
+    _assert_close(torch.stack([out[z, h] for z, h in heads]), ref, f"past 4 GiB causal={causal}")
+    # the kernel's LSE sums the rounded P: within 2^-11 relative of l, 1e-3 in ln
+    got_lse = torch.stack([lse[z, h] for z, h in heads]).cpu()
+    assert torch.allclose(got_lse, ref_lse, atol=1e-3, rtol=0), (got_lse - ref_lse).abs().max()
+    del q, k, v, out, lse
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_row_sum_adds_the_rounded_p(dtype):
     """fp16/bf16 kernels divide by the sum of the rounded P (the P that enters
