@@ -37,6 +37,12 @@ back-to-back calls, then the median of three windows of 10).  It is a
 yardstick of what this GPU sustains under the same power and clock conditions,
 not a baseline the kernel's figures are divided by.
 
+``power_during_headline`` (and ``power_during_warmup`` of C3 and of the
+GEMM) is one ``amd-smi metric --power --clock`` reading taken 0.8 of the way
+into that config's warm-up, while the launches go on: socket power and the
+GFX clocks of the eight XCDs.  Under this load the board sits at its power
+cap and the clock well below its 2400 MHz maximum.
+
 ``--calibrate-copy-mib M`` adds one plain device-to-device copy of M MiB after
 the timed work; under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` it gives
 the counter reading of a kernel with known traffic, which scales the readings
@@ -48,6 +54,8 @@ import json
 import math
 import os
 import platform
+import shutil
+import subprocess
 import sys
 import time
 
@@ -158,18 +166,75 @@ def resident_inputs(torch, cfg, keep_cpu=False):
     return dev, fp_ok, ((q_c, k_c, v_c) if keep_cpu else None)
 
 
-def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0, windows=1):
+def smi_start():
+    """Start one `amd-smi metric --power --clock` reading in a child process
+    (socket power and the per-XCD GFX clocks at that moment), or None when the
+    tool is not there."""
+    exe = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    if not os.path.exists(exe):
+        return None
+    try:
+        return subprocess.Popen([exe, "metric", "--power", "--clock", "--json"], stdout=subprocess.PIPE,
+                                stderr=subprocess.DEVNULL, text=True)
+    except OSError:
+        return None
+
+
+def smi_result(proc):
+    """The reading of smi_start's child: socket power (W) and GFX clocks (MHz)
+    of the one GPU it reports, or None (no tool, no parse, several GPUs)."""
+    if proc is None:
+        return None
+    try:
+        out, _ = proc.communicate(timeout=60)
+        gpus = json.loads(out)["gpu_data"]
+        if len(gpus) != 1:
+            return None
+        g = gpus[0]
+        gfx = [v["clk"]["value"] for k, v in sorted(g["clock"].items())
+               if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+        return {"socket_power_w": g["power"]["socket_power"]["value"],
+                "gfx_mhz_min": min(gfx), "gfx_mhz_max": max(gfx),
+                "gfx_mhz_mean": round(sum(gfx) / len(gfx), 1)}
+    except (subprocess.TimeoutExpired, ValueError, KeyError, TypeError):
+        proc.kill()
+        return None
+
+
+def sustained(torch, f, seconds, sample_power=False):
+    """Back-to-back calls of f() for about `seconds` (the device warm-up).
+    With sample_power, one amd-smi reading is taken 0.8 of the way in (the
+    process's first launches load the code objects, and the clock then ramps
+    under the load), while the calls go on until it returns; it is returned."""
+    f()  # the first call of a process loads the kernels: not part of the measured second
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    proc = None
+    while True:
+        el = time.perf_counter() - t
+        if sample_power and proc is None and el >= 0.8 * seconds:
+            proc = smi_start()
+            if proc is None:
+                sample_power = False
+        reading_pending = proc is not None and proc.poll() is None and el < seconds + 10
+        if el >= seconds and not reading_pending:
+            break
+        f()
+        torch.cuda.synchronize()
+    return smi_result(proc) if sample_power else None
+
+
+def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0, windows=1, sample_power=False):
     name, B, H, S, D, causal, scale, seed = cfg[:8]
     v8 = len(cfg) > 8 and cfg[8] == "e5m2"
     q, k, v = inputs
     BM, BN = F.get_tiling(B, H, S, D, causal)
+    power = None
     if device_warmup_s > 0:
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        while time.perf_counter() - t < device_warmup_s:
+        def burst():
             for _ in range(20):
                 F.attention(q, k, v, causal, scale, BM, BN)
-            torch.cuda.synchronize()
+        power = sustained(torch, burst, device_warmup_s, sample_power)
     for _ in range(warmup):
         F.attention(q, k, v, causal, scale, BM, BN)
     # attention() enqueues its kernel on the current stream: the events go there
@@ -196,6 +261,7 @@ def time_config(F, torch, cfg, inputs, fp_ok, steps, warmup, device_warmup_s=0.0
         "hbm_gbs_algorithmic": round(algo_bytes(B, H, S, D, causal, 1 if v8 else 2) / (ms * 1e-3) / 1e9, 1),
         "inputs_match_fingerprint": fp_ok,
         **({"v_dtype": "float8_e5m2"} if v8 else {}),
+        **({"power_during_warmup": power} if power is not None else {}),
     }
     return res
 
@@ -224,14 +290,11 @@ def roofline(cfg, res):
             "frac": round(achieved / peak, 4), "traffic": traffic, **src}
 
 
-def _median_window_ms(torch, f, warm_s, calls, windows=3):
+def _median_window_ms(torch, f, warm_s, calls, windows=3, sample_power=False):
     """Median over `windows` windows of `calls` back-to-back calls of f(), in ms
-    per call, after about `warm_s` seconds of back-to-back calls."""
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    while time.perf_counter() - t < warm_s:
-        f()
-        torch.cuda.synchronize()
+    per call, after about `warm_s` seconds of back-to-back calls (and the
+    amd-smi reading taken during them, with sample_power)."""
+    power = sustained(torch, f, warm_s, sample_power)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     stream = torch.cuda.current_stream()
     win = []
@@ -243,7 +306,8 @@ def _median_window_ms(torch, f, warm_s, calls, windows=3):
         e1.record(stream)
         torch.cuda.synchronize()
         win.append(e0.elapsed_time(e1) / calls)
-    return sorted(win)[(len(win) - 1) // 2]
+    ms = sorted(win)[(len(win) - 1) // 2]
+    return (ms, power) if sample_power else ms
 
 
 def gpu_reference(torch, sdpa_cases, warm_s=1.0):
@@ -258,9 +322,10 @@ def gpu_reference(torch, sdpa_cases, warm_s=1.0):
     n = 8192
     a = torch.randn(n, n, device="cuda", dtype=torch.float16)
     b = torch.randn(n, n, device="cuda", dtype=torch.float16)
-    ms = _median_window_ms(torch, lambda: a @ b, warm_s, 10)
+    ms, power = _median_window_ms(torch, lambda: a @ b, warm_s, 10, sample_power=True)
     out["gemm_fp16"] = {"shape": [n, n, n], "ms_per_call": round(ms, 4),
-                        "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)}
+                        "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1),
+                        **({"power_during_warmup": power} if power is not None else {})}
     del a, b
     try:
         from torch.nn.attention import SDPBackend, sdpa_kernel
@@ -400,7 +465,8 @@ def main():
         key = FINGERPRINT_KEY.get(cfg[0], cfg[0]) + ("-" + cfg[8] if len(cfg) > 8 else "")
         dev, fp_ok = resident[key]
         results[cfg[0]] = time_config(F, torch, cfg, dev, fp_ok, args.steps, args.warmup,
-                                      device_warmup_s=args.device_warmup_s, windows=args.windows)
+                                      device_warmup_s=args.device_warmup_s, windows=args.windows,
+                                      sample_power=cfg[0] in (HEADLINE, CAUSAL_TARGET))
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
     gref = None
     if not args.no_gpu_reference:
@@ -441,6 +507,9 @@ def main():
                    "layout": "[B,H,S,D]", "tiling": r["tiling"], "parallelism": "single GPU"},
         "pct_peak": r["pct_peak"],
         "roofline": roofline(cfg, r),
+        # one amd-smi reading (socket power, GFX clocks) during the headline's
+        # steady-state warm-up: the board's power cap sets the clock under this load
+        "power_during_headline": r.get("power_during_warmup"),
         "device_warmup_s": args.device_warmup_s,
         "configs": results,
     }

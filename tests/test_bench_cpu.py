@@ -107,3 +107,33 @@ def test_median_window_is_reported():
     res = bench.time_config(fake_F, fake_torch, cfg, (None, None, None), True, steps=10, warmup=2, windows=3)
     assert len(calls) == 2 + 3 * 10
     assert res["windows_ms"] == [1.2, 3.0, 1.0] and res["ms_per_call"] == 1.2
+
+
+class _FakeSmi:
+    """Stands in for the amd-smi child process: communicate() returns its JSON."""
+
+    def __init__(self, text):
+        self.text = text
+
+    def communicate(self, timeout=None):
+        return self.text, ""
+
+    def kill(self):
+        pass
+
+
+def _smi_json(n_gpus, power=1400, clocks=(1578, 1553, 1582, 1543, 1580, 1549, 1580, 1549)):
+    gpu = {"gpu": 0, "power": {"socket_power": {"value": power, "unit": "W"}, "gfx_voltage": "N/A"},
+           "clock": {**{f"gfx_{i}": {"clk": {"value": c, "unit": "MHz"}, "min_clk": "N/A"}
+                        for i, c in enumerate(clocks)},
+                     "mem_0": {"clk": {"value": 2000, "unit": "MHz"}}, "fclk_0": "N/A"}}
+    return json.dumps({"gpu_data": [gpu] * n_gpus})
+
+
+def test_power_reading_parses_socket_power_and_gfx_clocks():
+    r = bench.smi_result(_FakeSmi(_smi_json(1)))
+    assert r == {"socket_power_w": 1400, "gfx_mhz_min": 1543, "gfx_mhz_max": 1582, "gfx_mhz_mean": 1564.2}
+    # not attributable (several GPUs), not parseable, or no tool: no reading
+    assert bench.smi_result(_FakeSmi(_smi_json(2))) is None
+    assert bench.smi_result(_FakeSmi("amd-smi: error")) is None
+    assert bench.smi_result(None) is None
