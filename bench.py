@@ -27,7 +27,7 @@ window 11 % slow among repeats) does not decide the figure.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--windows N] [--no-cpu]
                     [--only NAME] [--calibrate-copy-mib M] [--device-warmup-s S]
-                    [--no-gpu-reference]
+                    [--no-gpu-reference] [--no-power]
 
 ``gpu_reference`` puts the kernel's MFMA fraction in context: in the same run,
 after the timed configs, an fp16 8192^3 GEMM through torch.matmul (the vendor's
@@ -310,7 +310,7 @@ def _median_window_ms(torch, f, warm_s, calls, windows=3, sample_power=False):
     return (ms, power) if sample_power else ms
 
 
-def gpu_reference(torch, sdpa_cases, warm_s=1.0):
+def gpu_reference(torch, sdpa_cases, warm_s=1.0, sample_power=True):
     """What the vendor's own libraries reach on this GPU in the same run, as a
     yardstick for the MFMA fraction (not a baseline the kernel is measured
     against): an fp16 GEMM through torch.matmul (hipBLASLt), 8192^3, and
@@ -322,7 +322,8 @@ def gpu_reference(torch, sdpa_cases, warm_s=1.0):
     n = 8192
     a = torch.randn(n, n, device="cuda", dtype=torch.float16)
     b = torch.randn(n, n, device="cuda", dtype=torch.float16)
-    ms, power = _median_window_ms(torch, lambda: a @ b, warm_s, 10, sample_power=True)
+    ms, power = _median_window_ms(torch, lambda: a @ b, warm_s, 10, sample_power=True) if sample_power else (
+        _median_window_ms(torch, lambda: a @ b, warm_s, 10), None)
     out["gemm_fp16"] = {"shape": [n, n, n], "ms_per_call": round(ms, 4),
                         "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1),
                         **({"power_during_warmup": power} if power is not None else {})}
@@ -434,6 +435,8 @@ def main():
                     help="seconds of back-to-back launches before each config (0 under counter passes)")
     ap.add_argument("--no-gpu-reference", action="store_true",
                     help="skip the vendor GEMM / PyTorch SDPA yardstick measured after the configs")
+    ap.add_argument("--no-power", action="store_true",
+                    help="take no amd-smi power/clock reading (e.g. under a profiler)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the path shards by (batch, head) with no "
@@ -466,7 +469,7 @@ def main():
         dev, fp_ok = resident[key]
         results[cfg[0]] = time_config(F, torch, cfg, dev, fp_ok, args.steps, args.warmup,
                                       device_warmup_s=args.device_warmup_s, windows=args.windows,
-                                      sample_power=cfg[0] in (HEADLINE, CAUSAL_TARGET))
+                                      sample_power=not args.no_power and cfg[0] in (HEADLINE, CAUSAL_TARGET))
         print(f"[bench] {cfg[0]}: {results[cfg[0]]}", file=sys.stderr, flush=True)
     gref = None
     if not args.no_gpu_reference:
@@ -475,7 +478,7 @@ def main():
             if cfg[0] in (HEADLINE, CAUSAL_TARGET) and len(cfg) <= 8:
                 q, k, v = resident[FINGERPRINT_KEY.get(cfg[0], cfg[0])][0]
                 cases.append((cfg[0], q, k, v, cfg[5], cfg[6]))
-        gref = gpu_reference(torch, cases)
+        gref = gpu_reference(torch, cases, sample_power=not args.no_power)
         print(f"[bench] gpu reference: {gref}", file=sys.stderr, flush=True)
     resident.clear()
     torch.cuda.empty_cache()
