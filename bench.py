@@ -186,7 +186,7 @@ def smi_result(proc):
     if proc is None:
         return None
     try:
-        out, _ = proc.communicate(timeout=60)
+        out, _ = proc.communicate(timeout=15)
         gpus = json.loads(out)["gpu_data"]
         if len(gpus) != 1:
             return None
@@ -216,7 +216,7 @@ def sustained(torch, f, seconds, sample_power=False):
             proc = smi_start()
             if proc is None:
                 sample_power = False
-        reading_pending = proc is not None and proc.poll() is None and el < seconds + 10
+        reading_pending = proc is not None and proc.poll() is None and el < seconds + 5
         if el >= seconds and not reading_pending:
             break
         f()
