@@ -159,14 +159,14 @@ int32_t queue_count(int64_t num_heads, int64_t grid) {
 // whole pair, where single blocks served longest-first end closer together.
 // Makespans per queue in block-lengths, with Wq workgroups: pairs
 // ceil(heads * nmb / 2 / Wq) * (nmb + 1), single blocks about their total
-// work / Wq + 1/2; pairs win ties within 3 %.  Only for kernels that load the
-// next task's Q during the current one (`qbuf`): the others load Q at a
-// task's start, and in lockstep rounds every workgroup of the grid does so at
-// once (measured at D = 256: 0.5-0.8 % slower with pairs).  Only for an even
+// work / Wq + 1/2; pairs win ties within 3 %.  Every tile takes them: at head
+// dim 256, whose tasks load Q at their start, interleaved against single
+// blocks: B=64 H=8 S=1024 +1.2 % (8 % fewer bytes fetched past L2), B=128
+// S=2048 +2.0 %, B=16 S=2048 +4.3 %, B=8 S=4096 +5.5 %.  Only for an even
 // nmb, whose pairs are all whole (B=64 H=8 S=1792 D=128: 1.5 % slower with
 // the middle blocks alone).
-int32_t use_pairs(int64_t num_heads, int32_t nmb, int64_t grid, int32_t nq, bool qbuf) {
-    if (!qbuf || nmb < 2 || (nmb & 1)) return 0;
+int32_t use_pairs(int64_t num_heads, int32_t nmb, int64_t grid, int32_t nq) {
+    if (nmb < 2 || (nmb & 1)) return 0;
     const int64_t wq = grid / nq;                  // workgroups per queue
     const int64_t hq = (num_heads + nq - 1) / nq;  // heads of the fullest queue
     if (wq < 1) return 0;
@@ -554,8 +554,7 @@ static int fwd_launch(const rsfa_fwd_args* a, void* stream, void* ws, uint64_t w
         grid = std::max<int64_t>(grid, 1);
         p.nq = queue_count(p.num_heads, grid);
         p.pairs = causal && modes[li] == MODE_FUSED && !(a->flags & RSFA_FLAG_SINGLE_BLOCKS)
-                      ? use_pairs(p.num_heads, p.nmb, grid, p.nq,
-                                  uses_q_buffer(k->d, k->bn, k->nw, true, MODE_FUSED))
+                      ? use_pairs(p.num_heads, p.nmb, grid, p.nq)
                       : 0;
         p.ticket = !dynamic ? nullptr : tickets_given ? tickets : stream_ticket(ds, stream);
         void* args[] = {&p};

@@ -329,21 +329,26 @@ def test_dynamic_and_static_schedules_bitwise_equal(causal):
 
 
 # Causal shapes whose query blocks the library hands out in pairs (nmb-1-i,
-# then i, per ticket) on a 256-CU MI355X: head dims 64 and 128 (the Q-buffer
-# kernels), an even nmb, and pairs that fill whole rounds of the 32 workgroups
-# of each of the 8 queues (heads per queue * nmb / 2 a multiple of 32).  A
-# partial last block, bf16, and pairs over several rounds.
+# then i, per ticket) on a 256-CU MI355X: an even nmb, and pairs that fill
+# whole rounds of the workgroups of each of the 8 queues (heads per queue *
+# nmb / 2 a multiple of the queue's workgroups: 32 for the 8-wave tiles, 64 for
+# the 4-wave (128, 64) tile at two workgroups per CU).  Head dims 64, 128
+# (Q-buffer kernels) and 256 (Q loaded at the task's start), the 4-wave tile,
+# a partial last block, bf16, and pairs over several rounds.
 PAIR_SHAPES = [
-    (16, 8, 1024, 128, torch.float16),
-    (16, 8, 1900, 128, torch.float16),
-    (8, 8, 2048, 64, torch.float16),
-    (16, 8, 1024, 128, torch.bfloat16),
-    (32, 8, 2048, 128, torch.float16),
+    (16, 8, 1024, 128, torch.float16, 0, 0),
+    (16, 8, 1900, 128, torch.float16, 0, 0),
+    (8, 8, 2048, 64, torch.float16, 0, 0),
+    (16, 8, 1024, 128, torch.bfloat16, 0, 0),
+    (32, 8, 2048, 128, torch.float16, 0, 0),
+    (64, 8, 1024, 256, torch.float16, 0, 0),
+    (8, 8, 4096, 256, torch.bfloat16, 0, 0),
+    (16, 8, 2048, 128, torch.float16, 128, 64),
 ]
 
 
-@pytest.mark.parametrize("Z,H,N,D,dtype", PAIR_SHAPES)
-def test_causal_pairs_match_single_blocks_bitwise(Z, H, N, D, dtype):
+@pytest.mark.parametrize("Z,H,N,D,dtype,BM,BN", PAIR_SHAPES)
+def test_causal_pairs_match_single_blocks_bitwise(Z, H, N, D, dtype, BM, BN):
     """Pairs change only which workgroup runs a query block and when: the
     output is bitwise that of one block per task (RSFA_FLAG_SINGLE_BLOCKS),
     under the dynamic queue and the static order alike, and a second launch
@@ -352,10 +357,11 @@ def test_causal_pairs_match_single_blocks_bitwise(Z, H, N, D, dtype):
     q, k, v = A.make_inputs(Z, H, N, D, seed=N + D, dtype=dtype)
     qd, kd, vd = _to_gpu(q, k, v)
     scale = 1 / math.sqrt(D)
-    a = F.forward(qd, kd, vd, True, scale)
-    b = F.forward(qd, kd, vd, True, scale, single_blocks=True)
-    c = F.forward(qd, kd, vd, True, scale, static_schedule=True)
-    d = F.forward(qd, kd, vd, True, scale)
+    print(f"pairs Z={Z} H={H} N={N} D={D} {dtype} tile=({BM},{BN})", flush=True)
+    a = F.forward(qd, kd, vd, True, scale, BM, BN)
+    b = F.forward(qd, kd, vd, True, scale, BM, BN, single_blocks=True)
+    c = F.forward(qd, kd, vd, True, scale, BM, BN, static_schedule=True)
+    d = F.forward(qd, kd, vd, True, scale, BM, BN)
     torch.cuda.synchronize()
     assert torch.equal(a, b), "pairs and single blocks differ"
     assert torch.equal(a, c) and torch.equal(a, d), "pair schedules differ"
