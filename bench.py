@@ -291,9 +291,10 @@ def roofline(cfg, res):
 
 
 def _median_window_ms(torch, f, warm_s, calls, windows=3, sample_power=False):
-    """Median over `windows` windows of `calls` back-to-back calls of f(), in ms
-    per call, after about `warm_s` seconds of back-to-back calls (and the
-    amd-smi reading taken during them, with sample_power)."""
+    """(ms, power): the median over `windows` windows of `calls` back-to-back
+    calls of f(), in ms per call, after about `warm_s` seconds of back-to-back
+    calls, and the amd-smi reading taken during those (None without
+    sample_power)."""
     power = sustained(torch, f, warm_s, sample_power)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     stream = torch.cuda.current_stream()
@@ -306,8 +307,7 @@ def _median_window_ms(torch, f, warm_s, calls, windows=3, sample_power=False):
         e1.record(stream)
         torch.cuda.synchronize()
         win.append(e0.elapsed_time(e1) / calls)
-    ms = sorted(win)[(len(win) - 1) // 2]
-    return (ms, power) if sample_power else ms
+    return sorted(win)[(len(win) - 1) // 2], power
 
 
 def gpu_reference(torch, sdpa_cases, warm_s=1.0, sample_power=True):
@@ -322,8 +322,7 @@ def gpu_reference(torch, sdpa_cases, warm_s=1.0, sample_power=True):
     n = 8192
     a = torch.randn(n, n, device="cuda", dtype=torch.float16)
     b = torch.randn(n, n, device="cuda", dtype=torch.float16)
-    ms, power = _median_window_ms(torch, lambda: a @ b, warm_s, 10, sample_power=True) if sample_power else (
-        _median_window_ms(torch, lambda: a @ b, warm_s, 10), None)
+    ms, power = _median_window_ms(torch, lambda: a @ b, warm_s, 10, sample_power=sample_power)
     out["gemm_fp16"] = {"shape": [n, n, n], "ms_per_call": round(ms, 4),
                         "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1),
                         **({"power_during_warmup": power} if power is not None else {})}
@@ -339,7 +338,7 @@ def gpu_reference(torch, sdpa_cases, warm_s=1.0, sample_power=True):
         try:
             with ctx():
                 f = lambda: TF.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=scale)  # noqa: E731
-                ms = _median_window_ms(torch, f, warm_s, 10)
+                ms, _ = _median_window_ms(torch, f, warm_s, 10)
             out["sdpa_" + name] = {"backend": backend, "ms_per_call": round(ms, 4),
                                    "tflops": round(flops(B, H, S, D, causal) / (ms * 1e-3) / 1e12, 1)}
         except Exception as e:  # e.g. no kernel of that backend for this GPU or shape
