@@ -3,8 +3,10 @@ and key tiles, one to thousands of keys), every head dim, fp16 / bf16 /
 float8-V, causal or not, scales of either sign, a tile request or none, the
 scheduling and split flags, and strided [B, S, H, D] views, each case against
 the oracle's closed form.  The case list is drawn once from a fixed seed, so a
-failure names a reproducible case."""
+failure names a reproducible case.  RSFA_SWEEP_CASES and RSFA_SWEEP_SEED
+draw a longer or another list (default: 200 cases, seed 20261202)."""
 import math
+import os
 import random
 
 import pytest
@@ -46,7 +48,8 @@ def _draw_cases(n, seed=20261202):
     return cases
 
 
-CASES = _draw_cases(200)
+CASES = _draw_cases(int(os.environ.get("RSFA_SWEEP_CASES", "200")),
+                    seed=int(os.environ.get("RSFA_SWEEP_SEED", "20261202")))
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"case{c['i']:02d}" for c in CASES])
